@@ -1,0 +1,111 @@
+/*
+ * miroxen_attn.h — C ABI of the MI355X (gfx950) DiT joint-attention library
+ * (libmiroxen_attn.so). Plain pointers, sizes and a hipStream_t passed as void*;
+ * no C++ or torch types. Every entry point returns 0 on success or a negative
+ * MX_E* code; mx_last_error() returns the message of the calling thread's last
+ * failure (thread-local, valid until that thread's next call).
+ *
+ * Tensor layouts follow the reference (src/kernels/attention.h:6-10):
+ *   q: [Sq, Hq, D], k/v: [Skv, Hkv, D], o: [Sq, Hq, D], bf16, token-major;
+ *   *_stride = elements between adjacent tokens (0 = dense H*D).
+ * All calls are stream-ordered and asynchronous (no host synchronisation) and
+ * run on the calling thread's current HIP device. The library allocates no
+ * device memory: the Sage path works in a caller-provided workspace.
+ */
+#ifndef MIROXEN_ATTN_H
+#define MIROXEN_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MX_OK = 0,
+  MX_E_INVALID = -1, /* argument rejected (reference: MX_CHECK -> std::runtime_error) */
+  MX_E_HIP = -2,     /* HIP runtime / launch error (reference: MX_CUDA / MX_KCHECK) */
+  MX_E_UNSUPPORTED = -3
+};
+
+/* Reference: struct AttnParams, src/kernels/attention.h:12-18. Same fields in the
+ * same order; kv_valid is new (key-padding mask) and sits last, so callers that
+ * zero-initialise the struct and set fields one by one keep working.
+ *   scale == 0 -> 1/sqrt(D); causal: query i sees keys [0, q_offset + i].
+ *   kv_valid: optional device pointer to uint8 [Skv], 0 = padded key (score -inf),
+ *   shared by all heads; NULL = every key valid. */
+typedef struct mx_attn_params {
+  int Sq, Skv, Hq, Hkv, D;
+  float scale;
+  int causal;
+  int q_offset;
+  int64_t q_stride, kv_stride, o_stride;
+  const uint8_t* kv_valid;
+} mx_attn_params;
+
+/* Reference: mx::flash_attn, src/kernels/attention.h:21-22 (impl attention.cu:409-417).
+ * D in {64,72,128}; bf16 in, fp32 accumulate, bf16 out. Invalid arguments ->
+ * MX_E_INVALID with the reference's validate() rules (attention.cu:350-369). */
+int mx_flash_attn(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
+                  void* stream);
+
+/* Reference: mx::flash_attn_fp8_workspace, src/kernels/attention.h:28 (attention_fp8.cu:471-473).
+ * Bytes of workspace flash_attn_fp8 needs (0 if the shape is empty). */
+size_t mx_flash_attn_fp8_workspace(const mx_attn_params* p);
+
+/* Reference: mx::flash_attn_fp8_supported, src/kernels/attention.h:30 (attention_fp8.cu:475-482).
+ * *supported = 1 when `device` is a gfx950 (INT8 + OCP-FP8 MFMA). */
+int mx_flash_attn_fp8_supported(int device, int* supported);
+
+/* Reference: mx::flash_attn_fp8_ok, src/kernels/attention.h:32 (attention_fp8.cu:451-459, 484-486).
+ * *ok = 1 when flash_attn_fp8 would take the quantized path for these arguments. */
+int mx_flash_attn_fp8_ok(const void* q, const void* k, const void* v, const void* o,
+                         const mx_attn_params* p, int* ok);
+
+/* Reference: mx::flash_attn_fp8, src/kernels/attention.h:33-34 (attention_fp8.cu:488-500).
+ * Sage attention: Q/K -> INT8 (Q per 16 tokens, K per 64 tokens after subtracting
+ * the per-channel K mean), V -> OCP e4m3 per channel, INT8 QK^T and FP8 PV MFMA,
+ * fp32 accumulation. ws: >= mx_flash_attn_fp8_workspace(p) bytes, 256-byte aligned.
+ * Falls back to mx_flash_attn when ws == NULL or flash_attn_fp8_ok is false.
+ * o may alias q (the main kernel reads only the workspace). */
+int mx_flash_attn_fp8(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
+                      void* ws, void* stream);
+
+/* Reference: mx::attn_reference, src/kernels/attention.h:37-38 (attention.cu:313-348, 419-423).
+ * Slow naive GPU attention (fp32 softmax), for tests only. */
+int mx_attn_reference(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
+                      void* stream);
+
+/* ---- Sage pieces, exposed for bit-exact parity tests and split timing ----
+ * No single reference counterpart: these are the two halves of
+ * flash_attn_fp8's run<D>() (src/kernels/attention_fp8.cu:422-449). */
+
+/* Byte offsets of the workspace regions (256-byte aligned each) and padded lengths.
+ *   qi [Hq][sq_pad][D] int8, ki [Hkv][skv_pad][D] int8, vt [Hkv][D][skv_pad] e4m3,
+ *   qs [Hq][sq_pad/16] f32, ks [Hkv][skv_pad/64] f32, km [Hkv][D] f32 (K mean),
+ *   va [Hkv][D] f32 (V abs-max), part: kv_stats partials. */
+typedef struct mx_sage_layout {
+  int64_t sq_pad, skv_pad;
+  size_t qi, ki, vt, qs, ks, km, va, part, total;
+} mx_sage_layout;
+int mx_sage_layout_of(const mx_attn_params* p, mx_sage_layout* out);
+
+/* Prologue only: kv_stats, Q/K INT8 quantization, V e4m3 quantization into ws. */
+int mx_sage_quantize(const void* q, const void* k, const void* v, const mx_attn_params* p, void* ws,
+                     void* stream);
+
+/* Main kernel only, on a workspace already filled by mx_sage_quantize. */
+int mx_sage_attend(void* o, const mx_attn_params* p, const void* ws, void* stream);
+
+/* Message of this thread's last failed call ("" if none). */
+const char* mx_last_error(void);
+
+/* Library build identifier (kernel variant string). */
+const char* mx_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIROXEN_ATTN_H */

@@ -1,0 +1,68 @@
+// Shared device/host helpers for the gfx950 attention kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "miroxen_attn.h"
+
+namespace mxa {
+
+using bf16x8 = __attribute__((ext_vector_type(8))) __bf16;
+using bf16x4 = __attribute__((ext_vector_type(4))) __bf16;
+using f32x16 = __attribute__((ext_vector_type(16))) float;
+using f32x4 = __attribute__((ext_vector_type(4))) float;
+using i32x16 = __attribute__((ext_vector_type(16))) int;
+using i32x8 = __attribute__((ext_vector_type(8))) int;
+using i32x4 = __attribute__((ext_vector_type(4))) int;
+using u32x4 = __attribute__((ext_vector_type(4))) unsigned;
+using u32x2 = __attribute__((ext_vector_type(2))) unsigned;
+
+#define MXA_LDS __attribute__((address_space(3)))
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLog2_448 = 8.807354922057604f;  // log2(448): FP8 P is stored as 448*p
+constexpr int kStatTok = 256;                     // tokens per kv_stats partial (reference kStatTok)
+constexpr int kSqPad = 256;                       // Sage Q rows are padded to this multiple
+constexpr int kKvPad = 64;                        // Sage key tile / K-scale group
+
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+
+// Round-to-nearest-even float -> bf16 bits.
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return uint32_t(f2bf(a)) | (uint32_t(f2bf(b)) << 16);
+}
+
+// Value of `x` from lane (lane ^ 32): v_permlane32_swap exchanges the upper half
+// of its first operand with the lower half of its second.
+__device__ __forceinline__ float other_half(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return __int_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+__device__ __forceinline__ int other_half_i(int x) {
+  auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return (threadIdx.x & 32) ? r[0] : r[1];
+}
+
+// 16-byte global -> LDS copy: lane i of the wave writes lds_wave_base + 16*i.
+__device__ __forceinline__ void g2lds16(const void* g, MXA_LDS void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, lds_wave_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Logical work-group index for a grid of n blocks such that consecutive logical
+// indices land on the same XCD (blocks are dispatched round-robin over 8 XCDs):
+// work items that share K/V (same head) then share one XCD's L2.
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+  const int q = n / 8, r = n % 8, x = b % 8, local = b / 8;
+  return x * q + (x < r ? x : r) + local;
+}
+
+}  // namespace mxa

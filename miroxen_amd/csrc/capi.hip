@@ -1,0 +1,229 @@
+// C-ABI entry points (declared in include/miroxen_attn.h). Host code only:
+// argument validation, path selection and launches. Errors never cross the ABI
+// as exceptions: every entry point returns a status and records a thread-local
+// message (reference contract: MX_CHECK throws std::runtime_error,
+// src/core/common.h:42-48; the C++ wrapper in include/miroxen/attention.h
+// rethrows).
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+
+#include "attn_common.hpp"
+
+namespace mxa {
+hipError_t launch_flash_bf16_d128(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*,
+                                  const mx_attn_params&, hipStream_t);
+hipError_t launch_naive_attn(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, const mx_attn_params&,
+                             hipStream_t);
+mx_sage_layout sage_layout(const mx_attn_params&);
+hipError_t launch_sage_quantize(const uint16_t*, const uint16_t*, const uint16_t*, const mx_attn_params&, char*,
+                                hipStream_t);
+hipError_t launch_sage_attend(uint16_t*, const mx_attn_params&, const char*, hipStream_t);
+}  // namespace mxa
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return MX_OK;
+  return fail(MX_E_HIP, "%s: HIP %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* x, uintptr_t a) { return (reinterpret_cast<uintptr_t>(x) & (a - 1)) == 0; }
+
+// Reference validate(), src/kernels/attention.cu:350-369: same rules and order;
+// fills dense strides and the default scale.
+int validate(const void* q, const void* k, const void* v, const void* o, const mx_attn_params* in,
+             mx_attn_params* out) {
+  if (!in) return fail(MX_E_INVALID, "attention: null parameter block");
+  mx_attn_params p = *in;
+  if (!(p.Sq > 0 && p.Skv > 0 && p.Hq > 0 && p.Hkv > 0 && p.Hq % p.Hkv == 0))
+    return fail(MX_E_INVALID, "attention: lengths/heads must be positive and Hq must be a multiple of Hkv");
+  if (!(p.D == 64 || p.D == 72 || p.D == 128))
+    return fail(MX_E_INVALID, "attention: unsupported head dimension %d", p.D);
+  if (!(p.causal == 0 || p.causal == 1)) return fail(MX_E_INVALID, "attention: causal must be 0 or 1");
+  if (!(q && k && v && o)) return fail(MX_E_INVALID, "attention: null tensor pointer");
+  if (!std::isfinite(p.scale)) return fail(MX_E_INVALID, "attention: scale must be finite");
+  const int64_t qdense = int64_t(p.Hq) * p.D, kdense = int64_t(p.Hkv) * p.D;
+  if (!p.q_stride) p.q_stride = qdense;
+  if (!p.kv_stride) p.kv_stride = kdense;
+  if (!p.o_stride) p.o_stride = qdense;
+  if (!(p.q_stride >= qdense && p.kv_stride >= kdense && p.o_stride >= qdense))
+    return fail(MX_E_INVALID, "attention: token stride is smaller than a row");
+  const int64_t limit = std::numeric_limits<int64_t>::max() / 2;
+  if (!(p.q_stride <= limit / p.Sq && p.kv_stride <= limit / p.Skv && p.o_stride <= limit / p.Sq))
+    return fail(MX_E_INVALID, "attention: tensor address range overflows");
+  if (p.Hq > 65535) return fail(MX_E_INVALID, "attention: too many heads for the launch grid");
+  if (p.scale == 0.f) p.scale = 1.f / std::sqrt(float(p.D));
+  *out = p;
+  return MX_OK;
+}
+
+// Reference with_defaults(), src/kernels/attention_fp8.cu:461-467.
+mx_attn_params with_defaults(mx_attn_params p) {
+  if (!p.q_stride) p.q_stride = int64_t(p.Hq) * p.D;
+  if (!p.kv_stride) p.kv_stride = int64_t(p.Hkv) * p.D;
+  if (!p.o_stride) p.o_stride = int64_t(p.Hq) * p.D;
+  if (p.scale == 0.f && p.D > 0) p.scale = 1.f / std::sqrt(float(p.D));
+  return p;
+}
+
+bool device_is_gfx950(int device) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return false;
+  return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+}
+
+// Reference fp8_ok(), src/kernels/attention_fp8.cu:451-459, for this build's
+// kernel: D == 128 only (D == 64 falls back to flash_attn), positive scale (the
+// integer row max assumes a positive score scale), and the device is gfx950.
+int fp8_ok(const void* q, const void* k, const void* v, const void* o, const mx_attn_params& p, bool* ok) {
+  *ok = false;
+  if (p.causal || p.D != 128 || p.Sq <= 0 || p.Skv <= 0 || p.Hkv <= 0 || p.Hq <= 0 || p.Hq % p.Hkv) return MX_OK;
+  if (p.q_stride % 8 || p.kv_stride % 8 || p.o_stride % 2 || !aligned(q, 16) || !aligned(k, 16) ||
+      !aligned(v, 16) || !aligned(o, 4))
+    return MX_OK;
+  if (!(p.scale > 0.f) || p.Hq > 65535) return MX_OK;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "flash_attn_fp8_ok");
+  *ok = device_is_gfx950(dev);
+  return MX_OK;
+}
+
+bool fast_bf16_ok(const void* q, const void* k, const void* v, const void* o, const mx_attn_params& p) {
+  return p.D == 128 && !p.causal && p.q_stride % 8 == 0 && p.kv_stride % 8 == 0 && p.o_stride % 2 == 0 &&
+         aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 4);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mx_last_error(void) { return g_err; }
+
+const char* mx_version(void) { return "miroxen_amd gfx950 bf16:w4q2k64 sage:w4q2k64"; }
+
+int mx_flash_attn(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p, void* stream) {
+  mx_attn_params a;
+  int rc = validate(q, k, v, o, p, &a);
+  if (rc) return rc;
+  auto s = static_cast<hipStream_t>(stream);
+  auto qq = static_cast<const uint16_t*>(q);
+  auto kk = static_cast<const uint16_t*>(k);
+  auto vv = static_cast<const uint16_t*>(v);
+  auto oo = static_cast<uint16_t*>(o);
+  if (fast_bf16_ok(q, k, v, o, a)) return hip_status(mxa::launch_flash_bf16_d128(qq, kk, vv, oo, a, s), "flash_attn");
+  return hip_status(mxa::launch_naive_attn(qq, kk, vv, oo, a, s), "flash_attn");
+}
+
+int mx_attn_reference(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p, void* stream) {
+  mx_attn_params a;
+  int rc = validate(q, k, v, o, p, &a);
+  if (rc) return rc;
+  return hip_status(mxa::launch_naive_attn(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                           static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), a,
+                                           static_cast<hipStream_t>(stream)),
+                    "attn_reference");
+}
+
+size_t mx_flash_attn_fp8_workspace(const mx_attn_params* p) {
+  if (!p || p->Sq <= 0 || p->Skv <= 0 || p->D <= 0 || p->Hq <= 0 || p->Hkv <= 0) return 0;
+  return mxa::sage_layout(*p).total;
+}
+
+int mx_sage_layout_of(const mx_attn_params* p, mx_sage_layout* out) {
+  if (!p || !out) return fail(MX_E_INVALID, "sage_layout: null argument");
+  if (p->Sq <= 0 || p->Skv <= 0 || p->D <= 0 || p->Hq <= 0 || p->Hkv <= 0)
+    return fail(MX_E_INVALID, "sage_layout: empty shape");
+  *out = mxa::sage_layout(*p);
+  return MX_OK;
+}
+
+int mx_flash_attn_fp8_supported(int device, int* supported) {
+  if (!supported) return fail(MX_E_INVALID, "flash_attn_fp8_supported: null output");
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess) return hip_status(e, "flash_attn_fp8_supported");
+  if (device < 0 || device >= count) return fail(MX_E_INVALID, "flash_attn_fp8_supported: no device %d", device);
+  *supported = device_is_gfx950(device) ? 1 : 0;
+  return MX_OK;
+}
+
+int mx_flash_attn_fp8_ok(const void* q, const void* k, const void* v, const void* o, const mx_attn_params* p,
+                         int* ok) {
+  if (!p || !ok) return fail(MX_E_INVALID, "flash_attn_fp8_ok: null argument");
+  bool b = false;
+  int rc = fp8_ok(q, k, v, o, with_defaults(*p), &b);
+  *ok = b ? 1 : 0;
+  return rc;
+}
+
+// Validation shared by the quantized entry points: the reference validate()
+// rules, then the fp8_ok() conditions, then the workspace contract.
+static int sage_args(const void* q, const void* k, const void* v, const void* o, const mx_attn_params* p,
+                     const void* ws, mx_attn_params* a, bool* ok) {
+  int rc = validate(q, k, v, o, p, a);
+  if (rc) return rc;
+  rc = fp8_ok(q, k, v, o, *a, ok);
+  if (rc || !*ok || !ws) return rc;
+  if (!aligned(ws, 256)) return fail(MX_E_INVALID, "flash_attn_fp8: workspace must be 256-byte aligned");
+  return MX_OK;
+}
+
+int mx_flash_attn_fp8(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p, void* ws,
+                      void* stream) {
+  mx_attn_params a;
+  bool ok = false;
+  int rc = sage_args(q, k, v, o, p, ws, &a, &ok);
+  if (rc) return rc;
+  if (!ws || !ok) return mx_flash_attn(q, k, v, o, p, stream);  // reference :491
+  auto s = static_cast<hipStream_t>(stream);
+  rc = hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                            static_cast<const uint16_t*>(v), a, static_cast<char*>(ws), s),
+                  "flash_attn_fp8 prologue");
+  if (rc) return rc;
+  return hip_status(mxa::launch_sage_attend(static_cast<uint16_t*>(o), a, static_cast<const char*>(ws), s),
+                    "flash_attn_fp8");
+}
+
+int mx_sage_quantize(const void* q, const void* k, const void* v, const mx_attn_params* p, void* ws,
+                     void* stream) {
+  mx_attn_params a;
+  bool ok = false;
+  int rc = sage_args(q, k, v, q, p, ws, &a, &ok);
+  if (rc) return rc;
+  if (!ok) return fail(MX_E_UNSUPPORTED, "sage_quantize: arguments not supported by the quantized path");
+  if (!ws) return fail(MX_E_INVALID, "sage_quantize: null workspace");
+  return hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                              static_cast<const uint16_t*>(v), a, static_cast<char*>(ws),
+                                              static_cast<hipStream_t>(stream)),
+                    "sage_quantize");
+}
+
+int mx_sage_attend(void* o, const mx_attn_params* p, const void* ws, void* stream) {
+  if (!p) return fail(MX_E_INVALID, "sage_attend: null parameter block");
+  if (!o || !ws) return fail(MX_E_INVALID, "sage_attend: null pointer");
+  mx_attn_params a;
+  // q/k/v are not read by the main kernel; the workspace stands in for them.
+  bool ok = false;
+  int rc = sage_args(ws, ws, ws, o, p, ws, &a, &ok);
+  if (rc) return rc;
+  if (!ok) return fail(MX_E_UNSUPPORTED, "sage_attend: arguments not supported by the quantized path");
+  return hip_status(mxa::launch_sage_attend(static_cast<uint16_t*>(o), a, static_cast<const char*>(ws),
+                                            static_cast<hipStream_t>(stream)),
+                    "sage_attend");
+}
+
+}  // extern "C"

@@ -1,0 +1,317 @@
+/*
+ * CPU oracle for the DiT joint-attention hot path. TEST INFRASTRUCTURE ONLY:
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
+ * this library, and only as the checker (or the timed CPU baseline). The
+ * product path (miroxen_amd/) never links or calls it.
+ *
+ * Every routine restates the reference algorithm in plain C; the reference
+ * file:line each one follows is cited beside it (paths are relative to the
+ * reference repository root). Build: oracle/Makefile (gcc, -ffp-contract=off so
+ * float expressions round exactly as written; no -ffast-math).
+ *
+ * Pinning (what fixes each routine independently of its own formula):
+ *  - or_attention_f64: closed form softmax(s*QK^T)V in double; pinned in
+ *    tests/test_oracle.py by a brute-force numpy float64 attention on tiny
+ *    shapes, one-hot/uniform special cases and the mask-compaction invariant.
+ *  - or_quant_rows / or_kv_stats: pinned by hand-worked vectors (amax=0,
+ *    +/-amax -> +/-127, half-way rounding to even, padded rows -> 0) and an
+ *    independent numpy restatement on random data.
+ *  - or_e4m3: pinned by the OCP FP8 table (all 256 codes decode/encode round
+ *    trip, half-way cases, saturation to 448, subnormals).
+ *  - or_sage_emulate: pinned by its limit: with exact (unquantized) P/V it must
+ *    equal or_attention_f64 to fp32 accuracy, and by the reference gate
+ *    (rel-RMS < 4 % vs exact attention, tests/attention_fp8_test.cpp:65).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---------- scalar helpers ---------- */
+
+float or_bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* float -> bf16, round to nearest even (NaN kept quiet). */
+uint16_t or_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+/* OCP FP8 E4M3FN encoder (OCP 8-bit Floating Point Specification v1.0):
+ * bias 7, no infinities, S.1111.111 = NaN, max finite 448. Round to nearest
+ * even, saturate finite overflow to +/-448 (the reference's __NV_SATFINITE
+ * conversion at src/kernels/attention_fp8.cu:119 and :187-188). */
+uint8_t or_e4m3(float x) {
+  if (isnan(x)) return 0x7f;
+  uint8_t s = signbit(x) ? 0x80 : 0;
+  double a = fabs((double)x);
+  if (a >= 448.0) return s | 0x7e;
+  /* quantum: 2^-9 in the subnormal range (a < 2^-6), else 2^(e-3) */
+  int e;
+  double q;
+  if (a < 0.015625) {
+    q = 1.0 / 512.0;
+  } else {
+    frexp(a, &e); /* a = m * 2^e, m in [0.5,1) -> floor(log2 a) = e-1 */
+    q = ldexp(1.0, e - 1 - 3);
+  }
+  double n = a / q;           /* exact: q is a power of two */
+  double r = floor(n);
+  double frac = n - r;
+  if (frac > 0.5 || (frac == 0.5 && fmod(r, 2.0) != 0.0)) r += 1.0;
+  double v = r * q;
+  if (v >= 448.0) return s | 0x7e;
+  if (v == 0.0) return s;
+  if (v < 0.015625) return s | (uint8_t)(v * 512.0);
+  frexp(v, &e);
+  int ex = e - 1;                                /* v in [2^ex, 2^(ex+1)) */
+  int m = (int)(v / ldexp(1.0, ex) * 8.0) - 8;   /* 3 mantissa bits */
+  return s | (uint8_t)(((ex + 7) << 3) | m);
+}
+
+float or_e4m3_to_f32(uint8_t c) {
+  int s = c & 0x80, e = (c >> 3) & 15, m = c & 7;
+  float v;
+  if (e == 15 && m == 7) return NAN;
+  if (e == 0) v = ldexpf((float)m, -9);
+  else v = ldexpf(1.0f + m / 8.0f, e - 7);
+  return s ? -v : v;
+}
+
+/* ---------- exact attention (double) ----------
+ * Restates tests/attention_test.cu:64-98 (cpu_oracle): double dot products,
+ * scale, subtract the row max, exp, normalise by the sum; 0 when the sum is 0.
+ * Extended with the key-padding mask (kv_valid[key]==0 -> weight 0), causal
+ * (key <= q_offset + row, tests/attention_test.cu:75) and GQA.
+ * rows: the query rows to evaluate (n_rows of them); out: [n_rows][Hq][D] f32. */
+void or_attention_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                      int Sq, int Skv, int Hq, int Hkv, int D, float scale,
+                      int causal, int q_offset, int64_t q_stride, int64_t kv_stride,
+                      const uint8_t* kv_valid, const int* rows, int n_rows, float* out,
+                      int threads) {
+  (void)Sq;
+  double sc = scale == 0.f ? 1.0 / sqrt((double)D) : (double)scale;
+  int group = Hq / Hkv;
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
+  for (int64_t job = 0; job < (int64_t)n_rows * Hq; ++job) {
+    int ri = (int)(job / Hq), head = (int)(job % Hq);
+    int row = rows[ri], kvh = head / group;
+    int64_t end = Skv;
+    if (causal) {
+      int64_t last = (int64_t)q_offset + row + 1;
+      end = last < 0 ? 0 : (last < Skv ? last : Skv);
+    }
+    double* w = (double*)malloc(sizeof(double) * (end > 0 ? end : 1));
+    double* acc = (double*)calloc(D, sizeof(double));
+    double mx = -INFINITY, sum = 0.0;
+    const uint16_t* qr = q + (int64_t)row * q_stride + (int64_t)head * D;
+    for (int64_t key = 0; key < end; ++key) {
+      if (kv_valid && !kv_valid[key]) { w[key] = -INFINITY; continue; }
+      const uint16_t* kr = k + key * kv_stride + (int64_t)kvh * D;
+      double dot = 0.0;
+      for (int d = 0; d < D; ++d) dot += (double)or_bf16_to_f32(qr[d]) * or_bf16_to_f32(kr[d]);
+      w[key] = dot * sc;
+      if (w[key] > mx) mx = w[key];
+    }
+    for (int64_t key = 0; key < end; ++key) {
+      double e = w[key] == -INFINITY ? 0.0 : exp(w[key] - mx);
+      w[key] = e;
+      sum += e;
+    }
+    for (int64_t key = 0; key < end; ++key) {
+      if (w[key] == 0.0) continue;
+      const uint16_t* vr = v + key * kv_stride + (int64_t)kvh * D;
+      for (int d = 0; d < D; ++d) acc[d] += w[key] * or_bf16_to_f32(vr[d]);
+    }
+    float* o = out + ((int64_t)ri * Hq + head) * D;
+    for (int d = 0; d < D; ++d) o[d] = sum > 0.0 ? (float)(acc[d] / sum) : 0.f;
+    free(w);
+    free(acc);
+  }
+}
+
+/* ---------- Sage prologue ---------- */
+
+/* K per-channel mean and V per-channel abs-max.
+ * Restates src/kernels/attention_fp8.cu:51-62 (kv_stats_kernel) with the
+ * summation order fixed: s_b is a sequential float sum over block b's <= 256
+ * tokens (:56-58), and kmean = sum over b ascending of (s_b / float(Skv))
+ * starting from 0.f (:60, one legal atomicAdd order; the exact order when
+ * Skv <= 256). vamax = max |v| (order independent, :61). */
+void or_kv_stats(const uint16_t* k, const uint16_t* v, int Skv, int Hkv, int D,
+                 int64_t kv_stride, float* kmean, float* vamax) {
+  for (int h = 0; h < Hkv; ++h)
+    for (int d = 0; d < D; ++d) {
+      float mean = 0.f, am = 0.f;
+      for (int64_t t0 = 0; t0 < Skv; t0 += 256) {
+        int64_t t1 = t0 + 256 < Skv ? t0 + 256 : Skv;
+        float s = 0.f;
+        for (int64_t t = t0; t < t1; ++t) {
+          s += or_bf16_to_f32(k[t * kv_stride + (int64_t)h * D + d]);
+          float a = fabsf(or_bf16_to_f32(v[t * kv_stride + (int64_t)h * D + d]));
+          am = a > am ? a : am;
+        }
+        mean += s / (float)Skv;
+      }
+      kmean[h * D + d] = mean;
+      vamax[h * D + d] = am;
+    }
+}
+
+/* Per-(head, G-row block) symmetric INT8 quantization.
+ * Restates src/kernels/attention_fp8.cu:65-100 (quant_rows_kernel):
+ * x' = bf16(x) - mean[c] (mean may be NULL), amax = max|x'| over the block,
+ * inv = amax > 0 ? 127.f/amax : 0, q = rint(x'*inv) (round half even,
+ * __float2int_rn at :96), scale = amax/127.f*mult (:99). Rows >= S are 0.
+ * out: [H][s_pad][D] int8, scale_out: [H][s_pad/G] f32. */
+void or_quant_rows(const uint16_t* x, int64_t stride, int S, int64_t s_pad, int H, int D, int G,
+                   const float* mean, float mult, int8_t* out, float* scale_out) {
+  float* buf = (float*)malloc(sizeof(float) * G * D);
+  for (int h = 0; h < H; ++h)
+    for (int64_t g = 0; g < s_pad / G; ++g) {
+      float am = 0.f;
+      for (int r = 0; r < G; ++r) {
+        int64_t row = g * G + r;
+        for (int c = 0; c < D; ++c) {
+          float f = 0.f;
+          if (row < S) {
+            f = or_bf16_to_f32(x[row * stride + (int64_t)h * D + c]);
+            if (mean) f = f - mean[h * D + c];
+          }
+          buf[r * D + c] = f;
+          float a = fabsf(f);
+          am = a > am ? a : am;
+        }
+      }
+      float inv = am > 0.f ? 127.f / am : 0.f;
+      for (int r = 0; r < G; ++r)
+        for (int c = 0; c < D; ++c) {
+          float p = buf[r * D + c] * inv;
+          out[((int64_t)h * s_pad + g * G + r) * D + c] = (int8_t)(int)nearbyintf(p);
+        }
+      scale_out[(int64_t)h * (s_pad / G) + g] = am / 127.f * mult;
+    }
+  free(buf);
+}
+
+/* V -> e4m3 with per-channel scale 448/amax, transposed to [H][D][skv_pad].
+ * Restates src/kernels/attention_fp8.cu:110-127 (v_quant_kernel): f = v*(448.f/a)
+ * when the key exists and a > 0, else 0; SATFINITE e4m3. Keys are stored in
+ * natural order (the reference's intra-32 key_pos permutation at :104-107 is an
+ * operand-layout detail of its MMA, not part of the values). */
+void or_v_quant(const uint16_t* v, int Skv, int Hkv, int D, int64_t kv_stride, int64_t skv_pad,
+                const float* vamax, uint8_t* vt) {
+  for (int h = 0; h < Hkv; ++h)
+    for (int d = 0; d < D; ++d) {
+      float a = vamax[h * D + d];
+      for (int64_t key = 0; key < skv_pad; ++key) {
+        float f = 0.f;
+        if (key < Skv && a > 0.f) f = or_bf16_to_f32(v[key * kv_stride + (int64_t)h * D + d]) * (448.f / a);
+        vt[((int64_t)h * D + d) * skv_pad + key] = or_e4m3(f);
+      }
+    }
+}
+
+/* ---------- Sage attention emulator ----------
+ * Scalar restatement of the arithmetic of src/kernels/attention_fp8.cu:286-416
+ * (fp8_attn_kernel, FP8 P.V path) over 64-key tiles:
+ *   s = sum_d qi*ki (int32, exact)                                  :286-304
+ *   sc = qs[row/16] * ks[tile]                                      :308
+ *   im = max over the tile's live keys (integers), next = max(m, im*sc)  :322-327
+ *   alpha = 2^(m - next) (0 on the first tile)                      :328
+ *   f = 2^(fma(s, sc, log2(448) - next)); dead keys -> 0            :331-338
+ *   l = l*alpha + sum f (unquantized f)                             :345
+ *   acc = acc*alpha + sum e4m3(f) * e4m3(vt)  (fp32 accumulate)     :352, :374-402
+ *   out = acc*vamax[d] * (1/(448*l)), 0 if l == 0                   :405-416
+ * "Dead" keys are keys >= Skv (the reference's tail, :309-316) and keys with
+ * kv_valid[key] == 0 (the build's key-padding mask). A tile with no live key for
+ * a row leaves m, l and acc unchanged. The exponent uses an fma of the exact
+ * int->float score instead of the reference's bit-trick sum (:331, :337): same
+ * value up to one fp32 rounding, which no reference test resolves.
+ * exp2 here is libm's double exp2 rounded to float (the GPU uses v_exp_f32,
+ * < 1 ulp). out: [n_rows][Hq][D] f32 (before the bf16 store). */
+void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, const float* qs,
+                     const float* ks, const float* vamax, int Sq, int Skv, int Hq, int Hkv, int D,
+                     int64_t sq_pad, int64_t skv_pad, const uint8_t* kv_valid, const int* rows,
+                     int n_rows, float* out, int threads) {
+  (void)Sq;
+  const int group = Hq / Hkv;
+  const float L448 = 8.807354922057604f;
+  float lut[256];
+  for (int c = 0; c < 256; ++c) lut[c] = or_e4m3_to_f32((uint8_t)c);
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
+  for (int64_t job = 0; job < (int64_t)n_rows * Hq; ++job) {
+    int ri = (int)(job / Hq), head = (int)(job % Hq), row = rows[ri], kvh = head / group;
+    const int8_t* qr = qi + ((int64_t)head * sq_pad + row) * D;
+    const float qscale = qs[(int64_t)head * (sq_pad / 16) + row / 16];
+    float m = -INFINITY, l = 0.f;
+    float* acc = (float*)calloc(D, sizeof(float));
+    int32_t s[64];
+    float f[64];
+    const int ntiles = (int)((Skv + 63) / 64);
+    for (int t = 0; t < ntiles; ++t) {
+      const float sc = qscale * ks[(int64_t)kvh * (skv_pad / 64) + t];
+      int live_any = 0;
+      int32_t im = INT32_MIN;
+      for (int j = 0; j < 64; ++j) {
+        int64_t key = (int64_t)t * 64 + j;
+        int live = key < Skv && (!kv_valid || kv_valid[key]);
+        const int8_t* kr = ki + ((int64_t)kvh * skv_pad + key) * D;
+        int32_t dot = 0;
+        for (int d = 0; d < D; ++d) dot += (int32_t)qr[d] * (int32_t)kr[d];
+        s[j] = live ? dot : INT32_MIN;
+        if (live) { live_any = 1; if (dot > im) im = dot; }
+      }
+      if (!live_any) continue;
+      float next = fmaxf(m, (float)im * sc);
+      float alpha = m == -INFINITY ? 0.f : (float)exp2((double)(m - next));
+      m = next;
+      float base = L448 - next, ts = 0.f;
+      for (int j = 0; j < 64; ++j) {
+        f[j] = s[j] == INT32_MIN ? 0.f : (float)exp2((double)fmaf((float)s[j], sc, base));
+        ts += f[j];
+      }
+      l = l * alpha + ts;
+      float p8[64];
+      for (int j = 0; j < 64; ++j) p8[j] = lut[or_e4m3(f[j])];
+      for (int d = 0; d < D; ++d) {
+        const uint8_t* vr = vt + ((int64_t)kvh * D + d) * skv_pad + (int64_t)t * 64;
+        float pv = 0.f;
+        for (int j = 0; j < 64; ++j) pv += p8[j] * lut[vr[j]];
+        acc[d] = acc[d] * alpha + pv;
+      }
+    }
+    float* o = out + ((int64_t)ri * Hq + head) * D;
+    for (int d = 0; d < D; ++d) {
+      float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
+      o[d] = acc[d] * vamax[kvh * D + d] * inv;
+    }
+    free(acc);
+  }
+}
+
+int or_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}

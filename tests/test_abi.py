@@ -1,0 +1,96 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the header
+declares, rejects the reference's invalid inputs before touching a device, and
+computes workspace sizes/layouts on the host. No kernel is launched here."""
+import ctypes
+import math
+import os
+import re
+
+import pytest
+
+from miroxen_amd import _lib
+from miroxen_amd.attention import AttnParams, flash_attn, attn_reference, flash_attn_fp8_workspace, sage_layout
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "miroxen_attn.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return set(re.findall(r"\b(mx_[a-z0-9_]+)\s*\(", src))
+
+
+def test_header_and_binding_agree():
+    assert _declared() == set(_lib.SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    for name in _declared():
+        assert hasattr(L, name), name
+    assert "gfx950" in L.mx_version().decode()
+
+
+def test_struct_layout_matches_header():
+    # int x5, float, int x2, int64 x3, pointer: 8 4-byte fields = 32 bytes, then 3*8 + 8
+    assert ctypes.sizeof(_lib.CParams) == 32 + 24 + 8
+    assert _lib.CParams.q_stride.offset == 32
+
+
+def _good():
+    return AttnParams(Sq=1, Skv=1, Hq=1, Hkv=1, D=64)
+
+
+# The reference's 11 invalid parameter sets x {flash_attn, attn_reference} + null q
+# (tests/attention_test.cu:178-208): 23 rejections.
+INVALID = [
+    dict(Sq=0), dict(Skv=-1), dict(Hq=3, Hkv=2), dict(D=80), dict(causal=2), dict(Hkv=0),
+    dict(q_stride=63), dict(kv_stride=-1), dict(o_stride=63), dict(scale=math.nan),
+    dict(kv_stride=2 ** 63 - 1),
+]
+
+
+@pytest.mark.parametrize("i", range(len(INVALID)))
+@pytest.mark.parametrize("fn", [flash_attn, attn_reference])
+def test_invalid_params_rejected(fn, i):
+    p = _good()
+    for key, val in INVALID[i].items():
+        setattr(p, key, val)
+    dummy = 256  # any non-null address: validation fails before it is used
+    with pytest.raises(RuntimeError):
+        fn(dummy, dummy, dummy, dummy, p, stream=0)
+
+
+def test_null_query_rejected():
+    with pytest.raises(RuntimeError, match="null tensor pointer"):
+        flash_attn(0, 256, 256, 256, _good(), stream=0)
+
+
+def test_error_message_is_reference_text():
+    p = _good(); p.D = 80
+    with pytest.raises(RuntimeError, match="unsupported head dimension 80"):
+        flash_attn(256, 256, 256, 256, p, stream=0)
+
+
+def test_too_many_heads_rejected():
+    p = AttnParams(Sq=1, Skv=1, Hq=65536, Hkv=1, D=128)
+    with pytest.raises(RuntimeError, match="too many heads"):
+        flash_attn(256, 256, 256, 256, p, stream=0)
+
+
+def test_workspace_and_layout():
+    assert flash_attn_fp8_workspace(AttnParams()) == 0
+    p = AttnParams(Sq=4352, Skv=4352, Hq=24, Hkv=24, D=128)
+    L = sage_layout(p)
+    assert L["sq_pad"] == 4352 and L["skv_pad"] == 4352
+    for name in ("qi", "ki", "vt", "qs", "ks", "km", "va", "part", "total"):
+        assert L[name] % 256 == 0
+    assert L["qi"] == 0 and L["ki"] == 24 * 4352 * 128 and L["vt"] == 2 * 24 * 4352 * 128
+    assert flash_attn_fp8_workspace(p) == L["total"]
+    assert L["total"] < 45e6  # config 2 workspace ~ 40 MB
+    p2 = AttnParams(Sq=1000, Skv=77, Hq=4, Hkv=2, D=128)
+    L2 = sage_layout(p2)
+    assert L2["sq_pad"] == 1024 and L2["skv_pad"] == 128
+    order = [L2[n] for n in ("qi", "ki", "vt", "qs", "ks", "km", "va", "part", "total")]
+    assert order == sorted(order)
+    assert L2["ki"] - L2["qi"] >= 4 * 1024 * 128 and L2["vt"] - L2["ki"] >= 2 * 128 * 128

@@ -1,0 +1,204 @@
+"""GPU parity of the Sage INT8/FP8 path (mx_sage_quantize / mx_sage_attend /
+mx_flash_attn_fp8 through the C ABI):
+ * the quantize prologue bit-exact against the oracle's restatement of the
+   reference quantizer (src/kernels/attention_fp8.cu:51-127);
+ * the attention kernel against the oracle's emulator of the reference
+   arithmetic (:286-416) fed the same workspace, and against exact FP32
+   attention (BASELINE: cosine >= 0.995; reference gate rel-RMS < 4 %,
+   tests/attention_fp8_test.cpp:65);
+ * the reference's fallback contract (:488-500)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from miroxen_amd import (AttnParams, flash_attn, flash_attn_fp8, flash_attn_fp8_ok, flash_attn_fp8_supported,
+                         flash_attn_fp8_workspace, sage_attend, sage_layout, sage_quantize)
+from miroxen_amd.synth import CONFIGS, make_inputs
+from tests.helpers import cosine, max_abs, query_rows, rel_rms
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _f32(t):
+    return t.float().cpu().numpy()
+
+
+def _ws(p, dev):
+    n = flash_attn_fp8_workspace(p)
+    return torch.zeros(n + 256, dtype=torch.uint8, device=dev)[:n] if n else None
+
+
+def _region(ws, L, name, count, dtype):
+    off = L[name]
+    return ws[off: off + count * np.dtype(dtype).itemsize].cpu().numpy().view(dtype)
+
+
+def _quantized(ws, p, L):
+    """Read the workspace regions back to host arrays."""
+    H, Hk, D = p.Hq, p.Hkv, p.D
+    sq, skv = L["sq_pad"], L["skv_pad"]
+    return dict(
+        qi=_region(ws, L, "qi", H * sq * D, np.int8).reshape(H, sq, D),
+        ki=_region(ws, L, "ki", Hk * skv * D, np.int8).reshape(Hk, skv, D),
+        vt=_region(ws, L, "vt", Hk * D * skv, np.uint8).reshape(Hk, D, skv),
+        qs=_region(ws, L, "qs", H * sq // 16, np.float32).reshape(H, sq // 16),
+        ks=_region(ws, L, "ks", Hk * skv // 64, np.float32).reshape(Hk, skv // 64),
+        km=_region(ws, L, "km", Hk * D, np.float32).reshape(Hk, D),
+        va=_region(ws, L, "va", Hk * D, np.float32).reshape(Hk, D),
+    )
+
+
+def _bias_inputs(Sq, Skv, Hq, Hkv, D, pad, kbias, dev, seed):
+    """The reference Sage test generator (tests/attention_fp8_test.cpp:18-27, :49-50):
+    N(0,1) plus a per-channel bias (kbias for K, 0.5 for V), strides padded by `pad`."""
+    rng = np.random.default_rng(seed)
+    qs, ks = Hq * D + pad, Hkv * D + pad
+    q = oracle.f32_to_bf16(rng.standard_normal((Sq, qs)).astype(np.float32))
+    kb = (rng.standard_normal(ks) * kbias).astype(np.float32)
+    k = oracle.f32_to_bf16((rng.standard_normal((Skv, ks)) + kb).astype(np.float32))
+    vb = (rng.standard_normal(ks) * 0.5).astype(np.float32)
+    v = oracle.f32_to_bf16((rng.standard_normal((Skv, ks)) + vb).astype(np.float32))
+    to = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(dev)
+    return to(q), to(k), to(v), qs, ks
+
+
+def test_supported(cuda):
+    assert flash_attn_fp8_supported(0)
+
+
+@pytest.mark.parametrize("Sq,Skv,Hq,Hkv,pad,kbias", [
+    (1, 1, 1, 1, 0, 0.0), (300, 300, 4, 4, 0, 0.0), (257, 1000, 4, 2, 0, 4.0), (130, 77, 2, 2, 8, 2.0),
+    (1088, 1088, 24, 24, 0, 8.0),
+])
+def test_prologue_bit_exact(cuda, Sq, Skv, Hq, Hkv, pad, kbias):
+    D = 128
+    print(f"prologue {Sq}x{Skv} H={Hq}/{Hkv} pad={pad}", flush=True)
+    q, k, v, qs, ks = _bias_inputs(Sq, Skv, Hq, Hkv, D, pad, kbias, cuda, Sq * 31 + Skv)
+    p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=D, q_stride=qs, kv_stride=ks, o_stride=qs)
+    ws = _ws(p, cuda)
+    sage_quantize(q, k, v, p, ws)
+    torch.cuda.synchronize()
+    L = sage_layout(p)
+    g = _quantized(ws, p, L)
+    _, want = oracle.sage_reference(_bits(q), _bits(k), _bits(v), Sq, Skv, Hq, Hkv, D, q_stride=qs, kv_stride=ks,
+                                    rows=np.zeros(0, np.int32))
+    for name in ("km", "va", "qs", "ks", "qi", "ki", "vt"):
+        assert np.array_equal(g[name], want[name]), f"{name} differs from the reference quantizer"
+
+
+def test_prologue_bit_exact_config3(cuda):
+    """Config 3 (outlier K channels, mask) at full size: every quantized byte and scale."""
+    cfg = CONFIGS[3]
+    q, k, v, mask = make_inputs(cfg, seed=3, device=cuda)
+    S, H = cfg.S, cfg.H
+    p = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128, kv_valid=mask)
+    ws = _ws(p, cuda)
+    sage_quantize(q, k, v, p, ws)
+    torch.cuda.synchronize()
+    g = _quantized(ws, p, sage_layout(p))
+    _, want = oracle.sage_reference(_bits(q), _bits(k), _bits(v), S, S, H, H, 128, rows=np.zeros(0, np.int32))
+    for name in ("km", "va", "qs", "ks", "qi", "ki", "vt"):
+        assert np.array_equal(g[name], want[name]), name
+
+
+def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
+    p = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128, kv_valid=mask)
+    ws = _ws(p, cuda)
+    o = torch.empty_like(q)
+    flash_attn_fp8(q, k, v, o, p, ws)
+    torch.cuda.synchronize()
+    L = sage_layout(p)
+    g = _quantized(ws, p, L)
+    rows = np.array(rows, np.int32)
+    mk = None if mask is None else mask.cpu().numpy()
+    emu = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128,
+                              kv_valid=mk, rows=rows)
+    exact = oracle.attention_f64(_bits(q), _bits(k), _bits(v), S, S, H, H, 128, kv_valid=mk, rows=rows)
+    got = _f32(o[torch.from_numpy(rows).long().to(cuda)])
+    c_emu, e_emu = cosine(got, emu), max_abs(got, emu)
+    c_ex, rr = cosine(got, exact), rel_rms(got, exact)
+    print(f"{seed_note} sage: cos(emu)={c_emu:.7f} maxabs(emu)={e_emu:.3g} cos(exact)={c_ex:.6f} relrms={rr:.4f}",
+          flush=True)
+    # emulator fed the same workspace: only accumulation order and the bf16 store differ
+    assert c_emu >= 0.99999 and e_emu <= 2e-2
+    assert c_ex >= 0.995 and rr < 0.04
+    return o
+
+
+@pytest.mark.parametrize("cfg_id", [1, 3, 4, 5])
+def test_sage_configs(cuda, cfg_id):
+    cfg = CONFIGS[cfg_id]
+    print(f"config {cfg_id} {cfg.name}", flush=True)
+    q, k, v, mask = make_inputs(cfg, seed=cfg_id, device=cuda)
+    rows = sorted(set(query_rows(cfg.S, cfg.H)) | set(range(0, cfg.S, max(1, cfg.S // 40))))
+    _sage_vs_oracle(cuda, q, k, v, mask, cfg.S, cfg.H, rows, f"config{cfg_id}")
+
+
+@pytest.mark.parametrize("Sq,Skv,Hq,Hkv,D,pad,kbias", [
+    (300, 300, 4, 4, 128, 0, 0.0), (257, 1000, 4, 2, 128, 0, 4.0), (130, 77, 2, 2, 64, 8, 2.0),
+    (1024, 4352, 2, 2, 128, 0, 8.0),
+])
+def test_reference_sage_cases(cuda, Sq, Skv, Hq, Hkv, D, pad, kbias):
+    """The reference's four Sage cases (tests/attention_fp8_test.cpp:110-113): rel-RMS < 4 %
+    against exact attention. D=64 takes the flash_attn fallback in this build."""
+    q, k, v, qs, ks = _bias_inputs(Sq, Skv, Hq, Hkv, D, pad, kbias, cuda, Sq * 31 + Skv)
+    p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=D, q_stride=qs if pad else 0, kv_stride=ks if pad else 0,
+                   o_stride=qs if pad else 0)
+    ws = _ws(p, cuda)
+    o = torch.zeros(Sq * qs, dtype=torch.bfloat16, device=cuda)
+    flash_attn_fp8(q, k, v, o, p, ws)
+    torch.cuda.synchronize()
+    exact = oracle.attention_f64(_bits(q), _bits(k), _bits(v), Sq, Skv, Hq, Hkv, D, q_stride=qs, kv_stride=ks)
+    got = _f32(o.view(Sq, qs)[:, : Hq * D]).reshape(exact.shape)
+    assert rel_rms(got, exact) < 0.04
+
+
+def test_fallbacks_and_aliasing(cuda):
+    S, H = 200, 2
+    q, k, v, qs, ks = _bias_inputs(S, S, H, H, 128, 0, 1.0, cuda, 9)
+    p = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128)
+    ref = torch.empty_like(q)
+    flash_attn(q, k, v, ref, p)
+    # no workspace -> flash_attn, bit for bit
+    o = torch.empty_like(q)
+    flash_attn_fp8(q, k, v, o, p, None)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), ref.view(torch.int16))
+    # causal or negative scale -> not the quantized path
+    assert flash_attn_fp8_ok(q, k, v, o, p)
+    assert not flash_attn_fp8_ok(q, k, v, o, AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128, causal=1))
+    assert not flash_attn_fp8_ok(q, k, v, o, AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128, scale=-0.1))
+    assert not flash_attn_fp8_ok(q, k, v, o, AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=64))
+    # o aliasing q: same result as a separate output
+    ws = _ws(p, cuda)
+    sep = torch.empty_like(q)
+    flash_attn_fp8(q, k, v, sep, p, ws)
+    qa = q.clone()
+    flash_attn_fp8(qa, k, v, qa, p, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(qa.view(torch.int16), sep.view(torch.int16))
+    # misaligned workspace is rejected
+    with pytest.raises(RuntimeError, match="256-byte aligned"):
+        flash_attn_fp8(q, k, v, o, p, ws.data_ptr() + 16)
+
+
+def test_sage_mask_equals_compacted_keys(cuda):
+    """Masked Sage == Sage over the compacted keys, up to quantization-grid effects
+    (K groups and the K mean shift with compaction), at config-2 size."""
+    cfg = CONFIGS[2]
+    q, k, v, mask = make_inputs(cfg, seed=22, device=cuda)
+    S, H = cfg.S, cfg.H
+    o1 = torch.empty_like(q); o2 = torch.empty_like(q)
+    p1 = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128, kv_valid=mask)
+    flash_attn_fp8(q, k, v, o1, p1, _ws(p1, cuda))
+    sel = mask.bool()
+    kc, vc = k[sel].contiguous(), v[sel].contiguous()
+    p2 = AttnParams(Sq=S, Skv=int(sel.sum()), Hq=H, Hkv=H, D=128)
+    flash_attn_fp8(q, kc, vc, o2, p2, _ws(p2, cuda))
+    torch.cuda.synchronize()
+    assert cosine(_f32(o1), _f32(o2)) > 0.999

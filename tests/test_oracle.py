@@ -1,0 +1,279 @@
+"""Pins the CPU oracle (oracle/oracle.c) against facts that do not come from its
+own formulas: the OCP FP8 table and nearest-value search, torch's bf16 rounding,
+a numpy float64 attention, closed-form special cases and invariants."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import cosine, rel_rms
+
+
+# ---------------- e4m3 (OCP FP8 E4M3FN) ----------------
+
+def _e4m3_table():
+    """Decode table straight from the OCP spec: e=0 subnormal m*2^-9, else (1+m/8)*2^(e-7);
+    S.1111.111 is NaN."""
+    vals = {}
+    for c in range(256):
+        s, e, m = c >> 7, (c >> 3) & 15, c & 7
+        if e == 15 and m == 7:
+            continue
+        v = m * 2.0 ** -9 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7)
+        vals[c] = -v if s else v
+    return vals
+
+
+def test_e4m3_decode_matches_spec_table():
+    for c, v in _e4m3_table().items():
+        assert oracle.e4m3_to_f32(c) == v, hex(c)
+    assert np.isnan(oracle.e4m3_to_f32(0x7F)) and np.isnan(oracle.e4m3_to_f32(0xFF))
+    assert max(_e4m3_table().values()) == 448.0
+
+
+def test_e4m3_roundtrip_all_codes():
+    for c, v in _e4m3_table().items():
+        assert oracle.e4m3(v) == c, (hex(c), v)
+
+
+def test_e4m3_is_nearest_even_by_search():
+    table = _e4m3_table()
+    codes = np.array([c for c in table if c != 0x80])  # +0 represents zero
+    vals = np.array([table[c] for c in codes])
+    rng = np.random.default_rng(7)
+    xs = np.concatenate([rng.uniform(-460, 460, 3000), rng.uniform(-0.03, 0.03, 2000),
+                         (vals[:-1] + np.diff(vals) / 2)[np.diff(vals) > 0]])  # all midpoints
+    for x in xs.astype(np.float32):
+        x = float(x)
+        d = np.abs(vals - x)
+        best = np.flatnonzero(d == d.min())
+        if len(best) > 1:  # tie: the even code (mantissa lsb 0) wins
+            best = [b for b in best if codes[b] & 1 == 0]
+        want = int(codes[best[0]])
+        if want == 0 and np.signbit(x):
+            want = 0x80
+        assert oracle.e4m3(x) == want, (x, hex(oracle.e4m3(x)), hex(want))
+
+
+def test_e4m3_saturates_and_subnormals():
+    assert oracle.e4m3(448.0) == 0x7E and oracle.e4m3(1e6) == 0x7E and oracle.e4m3(-1e6) == 0xFE
+    assert oracle.e4m3(470.0) == 0x7E  # SATFINITE, not NaN
+    assert oracle.e4m3(2.0 ** -9) == 0x01 and oracle.e4m3(2.0 ** -10) == 0x00  # tie -> even (0)
+    assert oracle.e4m3(1.5 * 2.0 ** -9) == 0x02  # tie between 1 and 2 -> even (2)
+    assert oracle.e4m3(1.0) == 0x38 and oracle.e4m3(-2.0) == 0xC0
+
+
+# ---------------- bf16 ----------------
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10,
+                        # exact ties: low 16 bits = 0x8000
+                        (rng.integers(0, 2 ** 16, 1000, dtype=np.uint32) << 16 | 0x8000).view(np.float32)])
+    x = x[np.isfinite(x)]
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(oracle.f32_to_bf16(x), want)
+    lib = oracle.lib()
+    for xv in x[:200]:
+        assert lib.or_f32_to_bf16(float(xv)) == oracle.f32_to_bf16(np.array([xv]))[0]
+
+
+# ---------------- exact attention ----------------
+
+def _np_attention(q, k, v, Hq, Hkv, D, scale, causal=0, q_offset=0, mask=None):
+    """Independent float64 attention with numpy (q [Sq,Hq,D], k/v [Skv,Hkv,D] float)."""
+    Sq, Skv = q.shape[0], k.shape[0]
+    out = np.zeros((Sq, Hq, D))
+    g = Hq // Hkv
+    for h in range(Hq):
+        s = q[:, h, :] @ k[:, h // g, :].T * scale
+        live = np.ones((Sq, Skv), bool)
+        if mask is not None:
+            live &= mask[None, :].astype(bool)
+        if causal:
+            live &= np.arange(Skv)[None, :] <= (q_offset + np.arange(Sq))[:, None]
+        s = np.where(live, s, -np.inf)
+        mx = s.max(1, keepdims=True)
+        mx = np.where(np.isfinite(mx), mx, 0)
+        w = np.where(live, np.exp(s - mx), 0)
+        den = w.sum(1, keepdims=True)
+        out[:, h, :] = np.where(den > 0, (w @ v[:, h // g, :]) / np.where(den > 0, den, 1), 0)
+    return out
+
+
+def _bf16_rand(rng, shape, mag=1.0):
+    return oracle.f32_to_bf16(rng.standard_normal(shape).astype(np.float32) * mag)
+
+
+@pytest.mark.parametrize("Sq,Skv,Hq,Hkv,D,causal,off,scale,masked", [
+    (7, 13, 2, 1, 64, 0, 0, 0.0, False),
+    (5, 40, 4, 2, 72, 1, 3, 0.0, False),
+    (9, 33, 2, 2, 128, 0, 0, -0.125, True),
+    (17, 65, 3, 1, 128, 1, -2, 0.3, True),
+])
+def test_attention_f64_matches_numpy(Sq, Skv, Hq, Hkv, D, causal, off, scale, masked):
+    rng = np.random.default_rng(Sq * 100 + Skv)
+    q = _bf16_rand(rng, (Sq, Hq, D), 2.0); k = _bf16_rand(rng, (Skv, Hkv, D), 2.0)
+    v = _bf16_rand(rng, (Skv, Hkv, D))
+    mask = (rng.random(Skv) > 0.3).astype(np.uint8) if masked else None
+    got = oracle.attention_f64(q, k, v, Sq, Skv, Hq, Hkv, D, scale, causal, off, kv_valid=mask)
+    sc = scale if scale != 0 else 1 / np.sqrt(D)
+    want = _np_attention(oracle.bf16_to_f32(q).reshape(Sq, Hq, D).astype(np.float64),
+                         oracle.bf16_to_f32(k).reshape(Skv, Hkv, D).astype(np.float64),
+                         oracle.bf16_to_f32(v).reshape(Skv, Hkv, D).astype(np.float64),
+                         Hq, Hkv, D, sc, causal, off, mask)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+def test_attention_f64_strided_rows():
+    rng = np.random.default_rng(3)
+    Sq, Skv, H, D, pad = 6, 11, 2, 64, 5
+    qs, ks = H * D + pad, H * D + pad + 2
+    q = _bf16_rand(rng, (Sq, qs)); k = _bf16_rand(rng, (Skv, ks)); v = _bf16_rand(rng, (Skv, ks))
+    got = oracle.attention_f64(q, k, v, Sq, Skv, H, H, D, q_stride=qs, kv_stride=ks, rows=[0, 3, 5])
+    dense = lambda t, S: t[:, : H * D].reshape(S, H * D)
+    want = oracle.attention_f64(dense(q, Sq), dense(k, Skv), dense(v, Skv), Sq, Skv, H, H, D, rows=[0, 3, 5])
+    np.testing.assert_array_equal(got, want)
+
+
+def test_attention_uniform_scores_give_mean_of_v():
+    rng = np.random.default_rng(4)
+    Skv, H, D = 50, 2, 128
+    q = np.zeros((3, H, D), np.uint16)  # q = 0 -> all scores equal
+    k = _bf16_rand(rng, (Skv, H, D)); v = _bf16_rand(rng, (Skv, H, D))
+    mask = np.ones(Skv, np.uint8); mask[::3] = 0
+    got = oracle.attention_f64(q, k, v, 3, Skv, H, H, D, kv_valid=mask)
+    vf = oracle.bf16_to_f32(v).reshape(Skv, H, D)[mask.astype(bool)].astype(np.float64).mean(0)
+    np.testing.assert_allclose(got, np.broadcast_to(vf, got.shape), rtol=1e-6, atol=1e-7)
+
+
+def test_attention_mask_equals_compacted_keys():
+    rng = np.random.default_rng(5)
+    Sq, Skv, H, D = 8, 70, 2, 128
+    q = _bf16_rand(rng, (Sq, H, D), 3.0); k = _bf16_rand(rng, (Skv, H, D), 3.0); v = _bf16_rand(rng, (Skv, H, D))
+    mask = (rng.random(Skv) > 0.4).astype(np.uint8)
+    sel = mask.astype(bool)
+    a = oracle.attention_f64(q, k, v, Sq, Skv, H, H, D, kv_valid=mask)
+    b = oracle.attention_f64(q, k[sel], v[sel], Sq, int(sel.sum()), H, H, D)
+    np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-7)
+
+
+def test_attention_all_masked_row_is_zero():
+    rng = np.random.default_rng(6)
+    q = _bf16_rand(rng, (2, 1, 64)); k = _bf16_rand(rng, (5, 1, 64)); v = _bf16_rand(rng, (5, 1, 64))
+    got = oracle.attention_f64(q, k, v, 2, 5, 1, 1, 64, kv_valid=np.zeros(5, np.uint8))
+    assert np.all(got == 0)
+
+
+# ---------------- Sage prologue ----------------
+
+def test_quant_rows_hand_vectors():
+    D, G = 128, 16
+    x = np.zeros((20, 1, D), np.float32)
+    x[0, 0, 0] = 127.0          # amax = 127 -> inv = 1
+    x[1, 0, :4] = [2.5, 3.5, -2.5, -127.0]   # ties round to even: 2, 4, -2; -amax -> -127
+    x[2, 0, 5] = 0.5            # tie -> 0
+    # second group (rows 16..19): all zero -> scale 0, q 0; rows >= S (20) padded to 32 -> 0
+    q, s = oracle.quant_rows(oracle.f32_to_bf16(x), D, 20, 32, 1, D, G, None, 2.0)
+    assert q[0, 0, 0] == 127 and list(q[0, 1, :4]) == [2, 4, -2, -127] and q[0, 2, 5] == 0
+    assert np.all(q[0, 16:] == 0)
+    assert s[0, 0] == np.float32(127.0) / np.float32(127.0) * np.float32(2.0) and s[0, 1] == 0.0
+
+
+def test_quant_rows_mean_and_scale_vs_numpy():
+    rng = np.random.default_rng(8)
+    S, H, D, G = 150, 3, 128, 64
+    xb = _bf16_rand(rng, (S, H, D), 3.0)
+    mean = rng.standard_normal((H, D)).astype(np.float32)
+    q, s = oracle.quant_rows(xb, H * D, S, 192, H, D, G, mean, 1.0)
+    xf = oracle.bf16_to_f32(xb).reshape(S, H, D)
+    xf = np.concatenate([xf - mean[None], np.zeros((192 - S, H, D), np.float32)]).astype(np.float32)
+    xf[S:] = 0
+    for h in range(H):
+        for g in range(192 // G):
+            blk = xf[g * G:(g + 1) * G, h, :]
+            am = np.float32(np.abs(blk).max())
+            inv = np.float32(127.0) / am if am > 0 else np.float32(0)
+            want = np.rint(blk * inv).astype(np.int8)
+            assert np.array_equal(q[h, g * G:(g + 1) * G], want)
+            assert s[h, g] == np.float32(am / np.float32(127.0) * np.float32(1.0))
+    assert np.all(np.abs(q.astype(int)) <= 127)
+
+
+def test_kv_stats_vs_numpy():
+    rng = np.random.default_rng(9)
+    for Skv in (200, 700):
+        H, D = 2, 128
+        k = _bf16_rand(rng, (Skv, H, D), 2.0); v = _bf16_rand(rng, (Skv, H, D))
+        km, va = oracle.kv_stats(k, v, Skv, H, D)
+        kf = oracle.bf16_to_f32(k).reshape(Skv, H, D); vf = oracle.bf16_to_f32(v).reshape(Skv, H, D)
+        want = np.zeros((H, D), np.float32)
+        for b in range(0, Skv, 256):
+            # np.cumsum in float32 is a sequential left-to-right float sum
+            part = np.cumsum(kf[b:b + 256], axis=0, dtype=np.float32)[-1]
+            want = (want + part / np.float32(Skv)).astype(np.float32)
+        assert np.array_equal(km, want)
+        assert np.array_equal(va, np.abs(vf).max(0))
+        np.testing.assert_allclose(km, kf.astype(np.float64).mean(0), atol=1e-5)
+
+
+def test_v_quant_layout_and_values():
+    rng = np.random.default_rng(10)
+    Skv, H, D = 70, 2, 128
+    v = _bf16_rand(rng, (Skv, H, D))
+    va = np.abs(oracle.bf16_to_f32(v).reshape(Skv, H, D)).max(0)
+    va[1, 7] = 0.0  # a zero channel quantizes to 0
+    vt = oracle.v_quant(v, Skv, H, D, H * D, 128, va)
+    assert vt.shape == (H, D, 128) and np.all(vt[:, :, Skv:] == 0) and np.all(vt[1, 7] == 0)
+    vf = oracle.bf16_to_f32(v).reshape(Skv, H, D)
+    for (h, d, key) in [(0, 0, 0), (1, 127, 69), (0, 64, 33)]:
+        assert vt[h, d, key] == oracle.e4m3(np.float32(vf[key, h, d]) * (np.float32(448) / va[h, d]))
+    # the channel max maps to +-448
+    h, d = 0, 5
+    key = int(np.argmax(np.abs(vf[:, h, d])))
+    assert vt[h, d, key] & 0x7F == 0x7E
+
+
+# ---------------- Sage emulator ----------------
+
+def test_sage_single_live_key_returns_dequantized_v():
+    rng = np.random.default_rng(11)
+    Sq, Skv, H, D = 3, 64, 1, 128
+    q = _bf16_rand(rng, (Sq, H, D)); k = _bf16_rand(rng, (Skv, H, D)); v = _bf16_rand(rng, (Skv, H, D))
+    mask = np.zeros(Skv, np.uint8); mask[37] = 1
+    out, t = oracle.sage_reference(q, k, v, Sq, Skv, H, H, D, kv_valid=mask)
+    # one live key: P = 448 exactly, l = 448 -> out = e4m3(v*448/a) * a / 448
+    deq = np.array([oracle.e4m3_to_f32(c) for c in t["vt"][0, :, 37]], np.float32) * t["va"][0] / np.float32(448)
+    np.testing.assert_allclose(out[:, 0, :], np.broadcast_to(deq, (Sq, D)), rtol=1e-6, atol=1e-7)
+
+
+def test_sage_uniform_scores_give_mean_of_dequantized_v():
+    rng = np.random.default_rng(12)
+    Sq, Skv, H, D = 2, 100, 1, 128
+    q = np.zeros((Sq, H, D), np.uint16)
+    k = _bf16_rand(rng, (Skv, H, D)); v = _bf16_rand(rng, (Skv, H, D))
+    out, t = oracle.sage_reference(q, k, v, Sq, Skv, H, H, D)
+    deq = np.vectorize(oracle.e4m3_to_f32)(t["vt"][0, :, :Skv]).astype(np.float64).mean(1) * t["va"][0] / 448
+    np.testing.assert_allclose(out[:, 0, :], np.broadcast_to(deq, (Sq, D)), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("Sq,Skv,Hq,Hkv,kbias,vbias", [
+    (300, 300, 4, 4, 0.0, 0.5),    # reference cases tests/attention_fp8_test.cpp:110-113 (scaled)
+    (257, 1000, 4, 2, 4.0, 0.5),
+    (200, 4352, 1, 1, 8.0, 0.5),
+])
+def test_sage_emulator_reference_gate(Sq, Skv, Hq, Hkv, kbias, vbias):
+    """rel-RMS < 4% against exact attention (tests/attention_fp8_test.cpp:65), with the
+    reference's per-channel K bias (and V bias) generator (:18-27)."""
+    rng = np.random.default_rng(Sq * 31 + Skv)
+    D = 128
+    q = _bf16_rand(rng, (Sq, Hq, D))
+    kb = rng.standard_normal(Hkv * D).astype(np.float32) * kbias
+    vb = rng.standard_normal(Hkv * D).astype(np.float32) * vbias
+    k = oracle.f32_to_bf16((rng.standard_normal((Skv, Hkv * D)) + kb).astype(np.float32))
+    v = oracle.f32_to_bf16((rng.standard_normal((Skv, Hkv * D)) + vb).astype(np.float32))
+    rows = np.arange(0, Sq, 7, dtype=np.int32)
+    out, _ = oracle.sage_reference(q, k, v, Sq, Skv, Hq, Hkv, D, rows=rows)
+    exact = oracle.attention_f64(q, k, v, Sq, Skv, Hq, Hkv, D, rows=rows)
+    assert rel_rms(out, exact) < 0.04
+    assert cosine(out, exact) > 0.995
