@@ -1,0 +1,156 @@
+"""Benchmark of the DiT joint-attention hot path on one MI355X.
+
+Workload (BASELINE.json metric "attention TFLOP/s + % MFMA peak at H=24,S=4352,D=128
+(BF16 and Sage INT8/FP8)"): config 2, Qwen-Image 1024^2 joint attention, B=1, H=24,
+S=4352, D=128, 200 of 256 text keys valid. A step is one attention call over that
+batch with inputs resident in HBM. `value` is the BF16 flash kernel's TFLOP/s
+(FLOP = 4*H*Sq*Skv*D, nominal Skv); the Sage INT8/FP8 path on config 3 (same shape,
+K outlier channels) is reported in the same line under "sage", end to end including
+its quantize prologue and kernel-only.
+
+Prints ONE JSON line. --gpus above 1 is refused: this build runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16 = 2500.0     # TFLOP/s, MI355X dense BF16 MFMA
+PEAK_FP8 = 5000.0      # TFLOP/s, dense FP8 (INT8 5.0 POP/s)
+PEAK_HBM = 8000.0      # GB/s
+
+
+def _time(fn, steps: int, warmup: int) -> float:
+    """Average ms per call over `steps` calls, HIP events on the stream the kernels use
+    (torch's current stream: the library launches on it)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(steps):
+        fn()
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def _traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (committed summary), or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def cpu_baseline(q, k, v, mask, S, H, D, budget_s: float = 12.0):
+    """The CPU oracle (C restatement of the reference's cpu_oracle, double accumulation,
+    OpenMP over (row, head)) timed on a bounded sample of query rows of the same workload."""
+    import numpy as np
+    import torch
+
+    import oracle
+    threads = min(os.cpu_count() or 1, 16)
+    bits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    qb, kb, vb = bits(q), bits(k), bits(v)
+    mk = None if mask is None else mask.cpu().numpy()
+    probe = np.arange(0, S, max(1, S // 16), dtype=np.int32)[:16]
+    t0 = time.perf_counter()
+    oracle.attention_f64(qb, kb, vb, S, S, H, H, D, kv_valid=mk, rows=probe, threads=threads)
+    dt = max(time.perf_counter() - t0, 1e-3)
+    n = int(min(S, max(16, len(probe) * budget_s / dt)))
+    rows = np.linspace(0, S - 1, n).astype(np.int32)
+    t0 = time.perf_counter()
+    oracle.attention_f64(qb, kb, vb, S, S, H, H, D, kv_valid=mk, rows=rows, threads=threads)
+    dt = time.perf_counter() - t0
+    flop = 4.0 * H * n * S * D
+    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{n} of {S} query rows x {H} heads, all {S} keys, {dt:.1f} s; "
+                      f"full call extrapolated {dt * S / n * 1e3:.0f} ms"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs the attention on one GPU only (no multi-GPU path); "
+              "use --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from miroxen_amd import (AttnParams, flash_attn, flash_attn_fp8, flash_attn_fp8_workspace, sage_attend,
+                             sage_quantize, version)
+    from miroxen_amd.synth import CONFIGS, attn_flops, make_inputs
+
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[2]
+    S, H, D = cfg.S, cfg.H, cfg.D
+    q, k, v, mask = make_inputs(cfg, seed=2, device=dev)
+    p = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=D, kv_valid=mask)
+    o = torch.empty_like(q)
+    flop = attn_flops(H, S, S, D)
+    eff_flop = attn_flops(H, S, int(mask.sum()), D)
+
+    t0 = time.perf_counter()
+    ms = _time(lambda: flash_attn(q, k, v, o, p), args.steps, args.warmup)
+    wall = time.perf_counter() - t0
+    tflops = flop / (ms * 1e-3) / 1e12
+
+    # ---- Sage INT8/FP8 on config 3 ----
+    c3 = CONFIGS[3]
+    q3, k3, v3, m3 = make_inputs(c3, seed=3, device=dev)
+    p3 = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=D, kv_valid=m3)
+    ws = torch.empty(flash_attn_fp8_workspace(p3), dtype=torch.uint8, device=dev)
+    o3 = torch.empty_like(q3)
+    ms_e2e = _time(lambda: flash_attn_fp8(q3, k3, v3, o3, p3, ws), args.steps, args.warmup)
+    ms_pro = _time(lambda: sage_quantize(q3, k3, v3, p3, ws), args.steps, args.warmup)
+    ms_main = _time(lambda: sage_attend(o3, p3, ws), args.steps, args.warmup)
+    pro_bytes = 9.0 * S * H * D  # read Q,K,V bf16 + write int8 Q, int8 K, fp8 V
+    sage = {
+        "workload": c3.name, "ms_end_to_end": round(ms_e2e, 4),
+        "tflops_end_to_end": round(flop / (ms_e2e * 1e-3) / 1e12, 2),
+        "ms_kernel": round(ms_main, 4), "tflops_kernel": round(flop / (ms_main * 1e-3) / 1e12, 2),
+        "frac_fp8_peak_kernel": round(flop / (ms_main * 1e-3) / 1e12 / PEAK_FP8, 4),
+        "speedup_vs_bf16_end_to_end": round(ms / ms_e2e, 3),
+        "prologue_ms": round(ms_pro, 4), "prologue_gbs": round(pro_bytes / (ms_pro * 1e-3) / 1e9, 1),
+        "prologue_frac_hbm": round(pro_bytes / (ms_pro * 1e-3) / 1e9 / PEAK_HBM, 4),
+        "dtype": "int8 QK^T / e4m3 PV, fp32 accumulate",
+    }
+
+    traffic = _traffic("flash_bf16_config2")
+    line = {
+        "metric": "attention TFLOP/s + % MFMA peak at H=24,S=4352,D=128 (BF16 and Sage INT8/FP8)",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded, config 2 distributions)",
+        "config": {"workload": cfg.name, "B": 1, "H": H, "Sq": S, "Skv": S, "D": D,
+                   "valid_keys": int(mask.sum()), "flop_nominal": flop, "flop_mask_effective": eff_flop,
+                   "kernel": version()},
+        "frac_bf16_peak": round(tflops / PEAK_BF16, 4),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16, 4), "traffic": traffic},
+        "sage": sage,
+        "timed_wall_s": round(wall, 3),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(q, k, v, mask, S, H, D)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
