@@ -27,16 +27,13 @@ constexpr int kKvPad = 64;                        // Sage key tile / K-scale gro
 
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
 
-// Round-to-nearest-even float -> bf16 bits.
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
-}
+// float -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return uint32_t(f2bf(a)) | (uint32_t(f2bf(b)) << 16);
+  using f32x2 = __attribute__((ext_vector_type(2))) float;
+  using bf16x2 = __attribute__((ext_vector_type(2))) __bf16;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
 }
 
 // Value of `x` from lane (lane ^ 32): v_permlane32_swap exchanges the upper half
@@ -56,6 +53,22 @@ __device__ __forceinline__ void g2lds16(const void* g, MXA_LDS void* lds_wave_ba
 }
 
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Key-liveness of one key per lane for a later tile: the in-range flag needs no
+// memory, the mask byte is loaded from a clamped index and only combined (in
+// key_live) when the tile is consumed, so the load never forces an early wait on
+// the tile prefetch issued next to it.
+struct KeyLive {
+  int in_range, byte;
+};
+__device__ __forceinline__ KeyLive key_live_load(const mx_attn_params& p, int key) {
+  KeyLive r;
+  r.in_range = key < p.Skv;
+  r.byte = 1;
+  if (p.kv_valid) r.byte = p.kv_valid[key < p.Skv ? key : p.Skv - 1];
+  return r;
+}
+__device__ __forceinline__ uint64_t key_live_ballot(const KeyLive& k) { return __ballot(k.in_range && k.byte); }
 
 // Logical work-group index for a grid of n blocks such that consecutive logical
 // indices land on the same XCD (blocks are dispatched round-robin over 8 XCDs):

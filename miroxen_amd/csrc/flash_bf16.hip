@@ -21,6 +21,13 @@
 //    XCD (and its L2).
 #include "attn_common.hpp"
 
+#ifndef MXA_BF16_NW
+#define MXA_BF16_NW 8
+#endif
+#ifndef MXA_BF16_QB
+#define MXA_BF16_QB 1
+#endif
+
 namespace mxa {
 
 namespace {
@@ -46,7 +53,11 @@ flash_bf16_d128(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                 const uint16_t* __restrict__ v, uint16_t* __restrict__ o, mx_attn_params p,
                 float c, uint32_t qsign) {
   constexpr int QW = 32 * QB, QT = NW * QW, NT = NW * 64;
-  extern __shared__ __align__(16) unsigned char smem[];
+  // Two distinct LDS objects (not one array indexed by stage) so the compiler can
+  // prove the in-flight global_load_lds into one buffer does not alias reads of the
+  // other, and does not wait for the prefetch before every LDS read.
+  __shared__ __align__(16) unsigned char lds0[2 * TILEB];
+  __shared__ __align__(16) unsigned char lds1[2 * TILEB];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 31, h = lane >> 5;
   const int ntq = (p.Sq + QT - 1) / QT;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
@@ -71,8 +82,7 @@ flash_bf16_d128(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
 
   // ---- K/V tile loader: each wave writes 64 consecutive 16-byte LDS slots per op ----
   const int64_t kvbase = int64_t(kvh) * D;
-  auto issue = [&](int t, int stage) {
-    unsigned char* kd = smem + stage * 2 * TILEB;
+  auto issue = [&](int t, unsigned char* kd) __attribute__((always_inline)) {
     unsigned char* vd = kd + TILEB;
     const int key0 = t * KT;
 #pragma unroll
@@ -98,8 +108,8 @@ flash_bf16_d128(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   }
 
   const int nt = (p.Skv + KT - 1) / KT;
-  issue(0, 0);
-  int live_next = lane < p.Skv && (!p.kv_valid || p.kv_valid[lane]);
+  issue(0, lds0);
+  KeyLive live_next = key_live_load(p, lane);
 
   // Per-lane LDS read offsets that do not depend on the tile.
   int koff[2][8];
@@ -115,17 +125,14 @@ flash_bf16_d128(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
   const int trow = (g16 >> 1) * 8 + (i16 >> 2);  // + kc*16 + r*4
   const int tcol = (g16 & 1) * 16 + (i16 & 3) * 4;  // + db*32 (elements)
 
-  for (int t = 0; t < nt; ++t) {
-    const int stage = t & 1;
+  auto tile = [&](int t, const unsigned char* kd, unsigned char* nxt) __attribute__((always_inline)) {
     wait_vm();
     __syncthreads();
-    const uint64_t live = __ballot(live_next);
+    const uint64_t live = key_live_ballot(live_next);
     if (t + 1 < nt) {
-      issue(t + 1, stage ^ 1);
-      const int key = (t + 1) * KT + lane;
-      live_next = key < p.Skv && (!p.kv_valid || p.kv_valid[key]);
+      issue(t + 1, nxt);
+      live_next = key_live_load(p, (t + 1) * KT + lane);
     }
-    const unsigned char* kd = smem + stage * 2 * TILEB;
     const unsigned char* vd = kd + TILEB;
 
     // ---- S^T = K Q^T ----
@@ -208,6 +215,10 @@ flash_bf16_d128(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
           acc[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[qb][kc], acc[qb][db], 0, 0, 0);
       }
     }
+  };
+  for (int t = 0; t < nt; t += 2) {
+    tile(t, lds0, lds1);
+    if (t + 1 < nt) tile(t + 1, lds1, lds0);
   }
 
   // ---- epilogue: O = acc / l -> bf16 ----
@@ -239,13 +250,13 @@ flash_bf16_d128(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
 // aligned with o_stride % 2 == 0.
 hipError_t launch_flash_bf16_d128(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                                   const mx_attn_params& p, hipStream_t s) {
-  constexpr int NW = 8, QB = 1, QT = NW * 32 * QB;
+  constexpr int NW = MXA_BF16_NW, QB = MXA_BF16_QB, QT = NW * 32 * QB;
   const float c = __builtin_fabsf(p.scale) * kLog2e;
   const uint32_t qsign = p.scale < 0.f ? 0x80008000u : 0u;
   const int ntq = (p.Sq + QT - 1) / QT;
   const int64_t blocks = int64_t(ntq) * p.Hq;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  const size_t lds = 2 * 2 * TILEB;
+  const size_t lds = 0;  // static LDS: two 32 KB K/V stages
   hipLaunchKernelGGL((flash_bf16_d128<NW, QB>), dim3(unsigned(blocks)), dim3(NW * 64), lds, s, q, k, v, o, p,
                      c, qsign);
   return hipGetLastError();

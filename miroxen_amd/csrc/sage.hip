@@ -10,6 +10,13 @@
 //   km [Hkv][D] f32 (K mean)   part [2][Hkv][nb][D] f32 (kv_stats partials, nb = ceil(Skv/256))
 #include "attn_common.hpp"
 
+#ifndef MXA_SAGE_NW
+#define MXA_SAGE_NW 8
+#endif
+#ifndef MXA_SAGE_QB
+#define MXA_SAGE_QB 1
+#endif
+
 namespace mxa {
 
 namespace {
@@ -192,7 +199,10 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
                const float* __restrict__ qs, const float* __restrict__ ks, const float* __restrict__ va,
                uint16_t* __restrict__ o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad) {
   constexpr int QW = 32 * QB, QT = NW * QW, NT = NW * 64;
-  extern __shared__ __align__(16) unsigned char smem[];
+  // Two distinct LDS objects so the prefetch into one provably does not alias reads
+  // of the other (no vmcnt wait before every LDS read).
+  __shared__ __align__(16) unsigned char lds0[KTILEB + VTILEB];
+  __shared__ __align__(16) unsigned char lds1[KTILEB + VTILEB];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 31, h = lane >> 5;
   const int ntq = (p.Sq + QT - 1) / QT;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
@@ -213,8 +223,7 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   }
   const float* kscale = ks + int64_t(kvh) * (skv_pad / KT);
 
-  auto issue = [&](int t, int stage) {
-    unsigned char* kd = smem + stage * (KTILEB + VTILEB);
+  auto issue = [&](int t, unsigned char* kd) __attribute__((always_inline)) {
     unsigned char* vd = kd + KTILEB;
     const int8_t* kg = ki + (int64_t(kvh) * skv_pad + int64_t(t) * KT) * D;
     const uint8_t* vg = vt + int64_t(kvh) * D * skv_pad + int64_t(t) * KT;
@@ -258,21 +267,18 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   }
 
   const int nt = (p.Skv + KT - 1) / KT;
-  issue(0, 0);
-  int live_next = lane < p.Skv && (!p.kv_valid || p.kv_valid[lane]);
+  issue(0, lds0);
+  KeyLive live_next = key_live_load(p, lane);
   constexpr int kDead = -2147483647 - 1;
 
-  for (int t = 0; t < nt; ++t) {
-    const int stage = t & 1;
+  auto tile = [&](int t, const unsigned char* kd, unsigned char* nxt) __attribute__((always_inline)) {
     wait_vm();
     __syncthreads();
-    const uint64_t live = __ballot(live_next);
+    const uint64_t live = key_live_ballot(live_next);
     if (t + 1 < nt) {
-      issue(t + 1, stage ^ 1);
-      const int key = (t + 1) * KT + lane;
-      live_next = key < p.Skv && (!p.kv_valid || p.kv_valid[key]);
+      issue(t + 1, nxt);
+      live_next = key_live_load(p, (t + 1) * KT + lane);
     }
-    const unsigned char* kd = smem + stage * (KTILEB + VTILEB);
     const unsigned char* vd = kd + KTILEB;
     const float ksc = kscale[t];
 
@@ -349,6 +355,10 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
       for (int qb = 0; qb < QB; ++qb)
         acc[qb][db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, pf[qb], acc[qb][db], 0, 0, 0, 0, 0, 0);
     }
+  };
+  for (int t = 0; t < nt; t += 2) {
+    tile(t, lds0, lds1);
+    if (t + 1 < nt) tile(t + 1, lds1, lds0);
   }
 
   // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----
@@ -423,13 +433,13 @@ hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint
 }
 
 hipError_t launch_sage_attend(uint16_t* o, const mx_attn_params& p, const char* ws, hipStream_t s) {
-  constexpr int NW = 8, QB = 1, QT = NW * 32 * QB;
+  constexpr int NW = MXA_SAGE_NW, QB = MXA_SAGE_QB, QT = NW * 32 * QB;
   static_assert(kSqPad % QT == 0, "Q padding must cover whole query tiles");
   const mx_sage_layout L = sage_layout(p);
   const int ntq = (p.Sq + QT - 1) / QT;
   const int64_t blocks = int64_t(ntq) * p.Hq;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  const size_t lds = 2 * (KTILEB + VTILEB);
+  const size_t lds = 0;  // static LDS: two 16 KB K/V stages
   hipLaunchKernelGGL((sage_attn_d128<NW, QB>), dim3(unsigned(blocks)), dim3(NW * 64), lds, s,
                      reinterpret_cast<const int8_t*>(ws + L.qi), reinterpret_cast<const int8_t*>(ws + L.ki),
                      reinterpret_cast<const uint8_t*>(ws + L.vt), reinterpret_cast<const float*>(ws + L.qs),
