@@ -54,6 +54,13 @@ __device__ __forceinline__ void g2lds16(const void* g, MXA_LDS void* lds_wave_ba
 
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Work-group barrier without __syncthreads()'s memory fence: the fence drains
+// every outstanding global load (vmcnt(0)), which would serialize a multi-stage
+// prefetch. Callers order LDS-DMA completion themselves with counted vmcnt waits;
+// LDS reads issued before the barrier have been consumed (their lgkmcnt waited)
+// before the barrier by construction.
+__device__ __forceinline__ void block_sync() { asm volatile("s_barrier" ::: "memory"); }
+
 // Key-liveness of one key per lane for a later tile: the in-range flag needs no
 // memory, the mask byte is loaded from a clamped index and only combined (in
 // key_live) when the tile is consumed, so the load never forces an early wait on
