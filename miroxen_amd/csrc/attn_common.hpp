@@ -77,6 +77,44 @@ __device__ __forceinline__ KeyLive key_live_load(const mx_attn_params& p, int ke
 }
 __device__ __forceinline__ uint64_t key_live_ballot(const KeyLive& k) { return __ballot(k.in_range && k.byte); }
 
+template <int N>
+__device__ __forceinline__ void wait_vm_n() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Liveness bitmaps of 64-key tiles (bit j = key t*64+j exists and is not
+// padding). With a key-padding mask they are built once per work-group into LDS
+// (table of kMaxLiveTiles entries, so masked calls need Skv <= 65536), so the
+// tile loop issues no per-tile mask loads; without a mask they are arithmetic.
+// Wave w handles tiles w, w+NW, ...; all of a wave's mask bytes are requested
+// before any is used.
+constexpr int kMaxLiveTiles = 1024;
+template <int NW, int KT>
+__device__ __forceinline__ void build_live(uint64_t* live, const mx_attn_params& p, int nt, int wave, int lane) {
+  if (!p.kv_valid) return;
+  constexpr int B = 8;  // tiles per batch per wave
+  for (int t0 = wave; t0 < nt; t0 += NW * B) {
+    int byte[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int t = t0 + j * NW, key = t * KT + lane;
+      byte[j] = t < nt && key < p.Skv ? int(p.kv_valid[key]) : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int t = t0 + j * NW;
+      const uint64_t bits = __ballot(byte[j] != 0);
+      if (t < nt && lane == 0) live[t] = bits;
+    }
+  }
+}
+template <int KT>
+__device__ __forceinline__ uint64_t tile_live(const uint64_t* live, const mx_attn_params& p, int t) {
+  if (p.kv_valid) return live[t];
+  const int left = p.Skv - t * KT;
+  return left >= 64 ? ~0ull : (1ull << left) - 1;
+}
+
 // Logical work-group index for a grid of n blocks such that consecutive logical
 // indices land on the same XCD (blocks are dispatched round-robin over 8 XCDs):
 // work items that share K/V (same head) then share one XCD's L2.

@@ -25,6 +25,9 @@ hipError_t launch_sage_attend(uint16_t*, const mx_attn_params&, const char*, hip
 
 namespace {
 
+// Masked calls keep one 64-bit liveness word per 64-key tile in LDS.
+constexpr int64_t kMaxMaskedSkv = 1024 * 64;
+
 thread_local char g_err[512] = "";
 
 int fail(int code, const char* fmt, ...) {
@@ -94,7 +97,7 @@ int fp8_ok(const void* q, const void* k, const void* v, const void* o, const mx_
   if (p.q_stride % 8 || p.kv_stride % 8 || p.o_stride % 2 || !aligned(q, 16) || !aligned(k, 16) ||
       !aligned(v, 16) || !aligned(o, 4))
     return MX_OK;
-  if (!(p.scale > 0.f) || p.Hq > 65535) return MX_OK;
+  if (!(p.scale > 0.f) || p.Hq > 65535 || (p.kv_valid && p.Skv > kMaxMaskedSkv)) return MX_OK;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_status(e, "flash_attn_fp8_ok");
@@ -104,7 +107,8 @@ int fp8_ok(const void* q, const void* k, const void* v, const void* o, const mx_
 
 bool fast_bf16_ok(const void* q, const void* k, const void* v, const void* o, const mx_attn_params& p) {
   return p.D == 128 && !p.causal && p.q_stride % 8 == 0 && p.kv_stride % 8 == 0 && p.o_stride % 2 == 0 &&
-         aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 4);
+         aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 4) &&
+         (!p.kv_valid || p.Skv <= kMaxMaskedSkv);
 }
 
 }  // namespace

@@ -67,11 +67,6 @@ constexpr int K_CHUNK = 2048, V_BLOCK = 4096;
 // Score-row -> key permutation inside a 32-key block: swap bits 2 and 3.
 __device__ __forceinline__ int perm32(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
-template <int N>
-__device__ __forceinline__ void wait_vm_n() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 // Per-lane constants.
 struct Lane {
   int lane, n, h;
@@ -275,30 +270,6 @@ __device__ __forceinline__ void store_block(const QBlock& X, uint16_t* o, const 
     }
 }
 
-// Liveness bitmaps of every 64-key tile (bit j = key t*64+j exists and is not
-// padding), built once per work-group into LDS so the tile loop issues no
-// per-tile mask loads. Wave w handles tiles w, w+NW, ...; all of a wave's mask
-// bytes are requested before any is used.
-constexpr int kMaxLiveTiles = 1024;  // Skv <= 65536 with a mask
-template <int NW>
-__device__ __forceinline__ void build_live(uint64_t* live, const mx_attn_params& p, int nt, int wave, int lane) {
-  constexpr int B = 8;  // tiles per batch per wave
-  for (int t0 = wave; t0 < nt; t0 += NW * B) {
-    int byte[B];
-#pragma unroll
-    for (int j = 0; j < B; ++j) {
-      const int t = t0 + j * NW, key = t * KT + lane;
-      byte[j] = t < nt && key < p.Skv ? (p.kv_valid ? int(p.kv_valid[key]) : 1) : 0;
-    }
-#pragma unroll
-    for (int j = 0; j < B; ++j) {
-      const int t = t0 + j * NW;
-      const uint64_t bits = __ballot(byte[j] != 0);
-      if (t < nt && lane == 0) live[t] = bits;
-    }
-  }
-}
-
 // ---------------- W8: 8 waves x 32 queries, two waves per SIMD ----------------
 // NS-stage K/V ring: tile t lives in stage t % NS; at the top of tile t the
 // loads of tile t + NS - 1 go into the stage tile t - 1 used. Each tile issues
@@ -345,7 +316,7 @@ flash_bf16_d128_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   issue(0, stage(std::integral_constant<int, 0>{}));
   if constexpr (NS > 2) if (1 < nt) issue(1, stage(std::integral_constant<int, 1>{}));
   if constexpr (NS > 3) if (2 < nt) issue(2, stage(std::integral_constant<int, 2>{}));
-  build_live<NW>(live_tiles, p, nt, wave, ln.lane);
+  build_live<NW, KT>(live_tiles, p, nt, wave, ln.lane);
   __syncthreads();  // bitmaps visible (once, before the pipelined loop)
 
   auto step = [&](int t, auto i) __attribute__((always_inline)) {
@@ -356,7 +327,7 @@ flash_bf16_d128_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
     if (t + NS - 2 < nt) wait_vm_n<(NS - 2) * OPS>();
     else wait_vm_n<0>();
     block_sync();
-    const uint64_t live = live_tiles[t];
+    const uint64_t live = tile_live<KT>(live_tiles, p, t);
     if (t + NS - 1 < nt) issue(t + NS - 1, stage(std::integral_constant<int, I + NS - 1>{}));
     scores(kd, A, ln);
     sched_k<0>();

@@ -8,14 +8,10 @@
 //   ki [Hkv][skv_pad][D] int8  ks [Hkv][skv_pad/64] f32 (K: 64-token groups, mean removed)
 //   vt [Hkv][D][skv_pad] e4m3  va [Hkv][D] f32          (V^T, per-channel 448/amax)
 //   km [Hkv][D] f32 (K mean)   part [2][Hkv][nb][D] f32 (kv_stats partials, nb = ceil(Skv/256))
+#include <type_traits>
+
 #include "attn_common.hpp"
 
-#ifndef MXA_SAGE_NW
-#define MXA_SAGE_NW 8
-#endif
-#ifndef MXA_SAGE_QB
-#define MXA_SAGE_QB 1
-#endif
 
 namespace mxa {
 
@@ -172,213 +168,235 @@ __global__ void __launch_bounds__(256) v_quant(const uint16_t* __restrict__ v, m
 
 // ---------------- main kernel ----------------
 //
-// Same skeleton as the BF16 kernel: one wave owns QB blocks of 32 queries, the
-// score MFMA computes S^T = K Q^T so each lane holds one query (per-lane softmax
-// state), K rows are permuted so each lane's score registers are the B operand
-// of the P*V MFMA directly: slot j of the 32-byte FP8 operand of wave half h is
-// key 32h + j of the 64-key tile. Integer row max, sc = qs*ks folded into one
-// FMA feeding v_exp_f32, P = e4m3(448*2^(...)), l from the unquantized values
-// (reference attention_fp8.cu:306-346).
+// Same skeleton as the BF16 kernel: 8 waves x 32 queries (two waves per SIMD);
+// the score MFMA computes S^T = K Q^T so each lane holds one query (per-lane
+// softmax state); K rows are permuted so each lane's score registers are the B
+// operand of the P*V MFMA directly: byte j of the 32-byte FP8 operand of wave
+// half h is key 32h + j of the 64-key tile. Integer row max; sc = qs*ks folded
+// into one FMA feeding v_exp_f32; P = e4m3(448 * 2^(s*sc - m - H)); l sums the
+// unquantized values (reference attention_fp8.cu:306-346).
+//
+// Lazy max with headroom H = kSageHeadroom (log2 units): the running max m only
+// moves when the tile max exceeds it by more than H, and P carries an extra
+// 2^-H so it never exceeds 448. The O rescale then becomes rare; the output is
+// unchanged up to rounding (softmax is invariant to the subtracted constant, and
+// acc and l carry the same factor). H = 0 is the reference's exact-max rule.
+//
+// LDS layouts (each tile 8 KB, DMA ops of 1 KB, read addresses = one or two
+// per-lane registers plus compile-time offsets, bank-conflict free):
+//   K int8: [4 d-chunks of 32][64 rows][2 halves of 16 B], half XOR row bit 5;
+//   V^T e4m3: [128 channel rows][64 B], 16-byte chunk XOR ((row >> 2) & 3).
 
 constexpr int KT = 64;
-constexpr int KROWB = D;              // int8 K row bytes
-constexpr int KTILEB = KT * KROWB;    // 8 KB
-constexpr int VROWB = KT;             // fp8 V^T row bytes (64 keys)
-constexpr int VTILEB = D * VROWB;     // 8 KB
+constexpr int KTILEB = KT * D;        // 8 KB int8 K tile
+constexpr int VTILEB = D * KT;        // 8 KB fp8 V^T tile
+constexpr int STAGEB = KTILEB + VTILEB;
+constexpr float kSageHeadroom = 2.f;
+#ifndef MXA_SAGE_NS
+#define MXA_SAGE_NS 2
+#endif
 
-__device__ __forceinline__ int swz_k(int r) { return (r & 3) | (((r >> 5) & 1) << 2); }
-__device__ __forceinline__ int swz_v(int r) { return (r >> 2) & 3; }
 // Score row m of key block kb -> key within the 64-key tile.
 __device__ __forceinline__ int kperm(int kb, int m) {
   return ((m >> 2) & 1) * 32 + kb * 16 + (m >> 3) * 4 + (m & 3);
 }
 
-template <int NW, int QB>
-__global__ void __launch_bounds__(NW * 64, 1)
+template <int NW>
+__device__ __forceinline__ void sage_load_tile(const int8_t* ki, const uint8_t* vt, int t, unsigned char* dst,
+                                               int kvh, int64_t skv_pad, int wave, int lane) {
+  const int8_t* kg = ki + (int64_t(kvh) * skv_pad + int64_t(t) * KT) * D;
+  const uint8_t* vg = vt + int64_t(kvh) * D * skv_pad + int64_t(t) * KT;
+#pragma unroll
+  for (int jj = 0; jj < 8 / NW; ++jj) {  // K: op j = d-chunk j/2, rows (j%2)*32 + lane/2
+    const int j = jj * NW + wave;
+    const int row = (j & 1) * 32 + (lane >> 1);
+    const int h = (lane & 1) ^ ((row >> 5) & 1);
+    g2lds16(kg + row * D + (j >> 1) * 32 + h * 16, (MXA_LDS void*)(dst + j * 1024));
+  }
+#pragma unroll
+  for (int jj = 0; jj < 8 / NW; ++jj) {  // V^T: op j = channel rows j*16 + lane/4
+    const int j = jj * NW + wave;
+    const int row = j * 16 + (lane >> 2);
+    const int lc = (lane & 3) ^ ((row >> 2) & 3);
+    g2lds16(vg + int64_t(row) * skv_pad + lc * 16, (MXA_LDS void*)(dst + KTILEB + j * 1024));
+  }
+}
+
+template <int NS>
+__global__ void __launch_bounds__(512, 1)
 sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, const uint8_t* __restrict__ vt,
                const float* __restrict__ qs, const float* __restrict__ ks, const float* __restrict__ va,
                uint16_t* __restrict__ o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad) {
-  constexpr int QW = 32 * QB, QT = NW * QW, NT = NW * 64;
-  // Two distinct LDS objects so the prefetch into one provably does not alias reads
-  // of the other (no vmcnt wait before every LDS read).
-  __shared__ __align__(16) unsigned char lds0[KTILEB + VTILEB];
-  __shared__ __align__(16) unsigned char lds1[KTILEB + VTILEB];
+  constexpr int NW = 8, QT = NW * 32, OPS = 2 * (8 / NW);
+  static_assert(NS >= 2 && NS <= 4, "2..4 stages");
+  __shared__ __align__(16) unsigned char st0[STAGEB];
+  __shared__ __align__(16) unsigned char st1[STAGEB];
+  __shared__ __align__(16) unsigned char st2[STAGEB];
+  __shared__ __align__(16) unsigned char st3[STAGEB];
+  __shared__ uint64_t live_tiles[kMaxLiveTiles];
+  auto stage = [&](auto i) __attribute__((always_inline)) -> unsigned char* {
+    constexpr int I = decltype(i)::value % NS;
+    if constexpr (I == 0) return st0;
+    else if constexpr (I == 1) return st1;
+    else if constexpr (I == 2) return st2;
+    else return st3;
+  };
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 31, h = lane >> 5;
   const int ntq = (p.Sq + QT - 1) / QT;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int head = L / ntq, qtile = L % ntq;
   const int kvh = head / (p.Hq / p.Hkv);
-  const int q0 = qtile * QT + wave * QW;
+  const int q0 = qtile * QT + wave * 32;
+  const int nt = (p.Skv + KT - 1) / KT;
+
+  auto issue = [&](int t, unsigned char* dst) __attribute__((always_inline)) {
+    sage_load_tile<NW>(ki, vt, t, dst, kvh, skv_pad, wave, lane);
+  };
+  issue(0, stage(std::integral_constant<int, 0>{}));
+  if constexpr (NS > 2) if (1 < nt) issue(1, stage(std::integral_constant<int, 1>{}));
+  if constexpr (NS > 3) if (2 < nt) issue(2, stage(std::integral_constant<int, 2>{}));
 
   // Q^T fragments: lane (n, h) holds 16 int8 channels 32c + 16h .. +15 of its query.
-  i32x4 qf[QB][4];
-  float qscale[QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int row = q0 + qb * 32 + n;  // < sq_pad (sq_pad is a multiple of QT)
+  const int row = q0 + n;  // < sq_pad (sq_pad is a multiple of QT)
+  i32x4 qf[4];
+  {
     const int8_t* src = qi + (int64_t(head) * sq_pad + row) * D + h * 16;
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) qf[qb][cc] = *reinterpret_cast<const i32x4*>(src + cc * 32);
-    qscale[qb] = qs[int64_t(head) * (sq_pad / 16) + row / 16];
+    for (int cc = 0; cc < 4; ++cc) qf[cc] = *reinterpret_cast<const i32x4*>(src + cc * 32);
   }
+  const float qscale = qs[int64_t(head) * (sq_pad / 16) + row / 16];
   const float* kscale = ks + int64_t(kvh) * (skv_pad / KT);
+  build_live<NW, KT>(live_tiles, p, nt, wave, lane);
+  __syncthreads();  // bitmaps visible (once, before the pipelined loop)
 
-  auto issue = [&](int t, unsigned char* kd) __attribute__((always_inline)) {
-    unsigned char* vd = kd + KTILEB;
-    const int8_t* kg = ki + (int64_t(kvh) * skv_pad + int64_t(t) * KT) * D;
-    const uint8_t* vg = vt + int64_t(kvh) * D * skv_pad + int64_t(t) * KT;
-#pragma unroll
-    for (int j = 0; j < (KTILEB / 16) / NT; ++j) {
-      const int slot0 = (j * NW + wave) * 64, slot = slot0 + lane;
-      const int r = slot >> 3, pc = slot & 7;
-      g2lds16(kg + r * KROWB + ((pc ^ swz_k(r)) << 4), (MXA_LDS void*)(kd + slot0 * 16));
-    }
-#pragma unroll
-    for (int j = 0; j < (VTILEB / 16) / NT; ++j) {
-      const int slot0 = (j * NW + wave) * 64, slot = slot0 + lane;
-      const int r = slot >> 2, pc = slot & 3;
-      g2lds16(vg + int64_t(r) * skv_pad + ((pc ^ swz_v(r)) << 4), (MXA_LDS void*)(vd + slot0 * 16));
-    }
-  };
+  // Per-lane LDS read bases.
+  const int krow = kperm(0, n);
+  const int kbase = krow * 32 + ((h ^ ((krow >> 5) & 1)) << 4);
+  const int vsw = (n >> 2) & 3;
+  const int vbase0 = KTILEB + n * 64 + (((2 * h) ^ vsw) << 4);
+  const int vbase1 = KTILEB + n * 64 + (((2 * h + 1) ^ vsw) << 4);
 
-  f32x16 acc[QB][4];
-  float m[QB], l[QB];
+  f32x16 acc[4];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    m[qb] = -__builtin_inff();
-    l[qb] = 0.f;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) acc[qb][db] = f32x16{};
-  }
-
-  int koff[2][4];
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    const int r = kperm(kb, n);
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) koff[kb][cc] = r * KROWB + (((2 * cc + h) ^ swz_k(r)) << 4);
-  }
-  int voff[4][2];
-#pragma unroll
-  for (int db = 0; db < 4; ++db) {
-    const int r = db * 32 + n;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) voff[db][u] = r * VROWB + (((2 * h + u) ^ swz_v(r)) << 4);
-  }
-
-  const int nt = (p.Skv + KT - 1) / KT;
-  issue(0, lds0);
-  KeyLive live_next = key_live_load(p, lane);
+  for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
+  float m = -__builtin_inff(), l = 0.f;
   constexpr int kDead = -2147483647 - 1;
 
-  auto tile = [&](int t, const unsigned char* kd, unsigned char* nxt) __attribute__((always_inline)) {
-    wait_vm();
-    __syncthreads();
-    const uint64_t live = key_live_ballot(live_next);
-    if (t + 1 < nt) {
-      issue(t + 1, nxt);
-      live_next = key_live_load(p, (t + 1) * KT + lane);
-    }
-    const unsigned char* vd = kd + KTILEB;
+  auto step = [&](int t, auto i) __attribute__((always_inline)) {
+    const unsigned char* sd = stage(i);
+    if (t + NS - 2 < nt) wait_vm_n<(NS - 2) * OPS>();
+    else wait_vm_n<0>();
+    block_sync();
+    const uint64_t live = tile_live<KT>(live_tiles, p, t);
+    if (t + NS - 1 < nt) issue(t + NS - 1, stage(std::integral_constant<int, decltype(i)::value + NS - 1>{}));
     const float ksc = kscale[t];
 
     // ---- S^T = K Q^T (int32, exact) ----
-    i32x16 s[QB][2];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) s[qb][0] = s[qb][1] = i32x16{};
+    i32x16 s[2];
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const i32x4 a = *reinterpret_cast<const i32x4*>(kd + koff[kb][cc]);
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-          s[qb][kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[qb][cc], s[qb][kb], 0, 0, 0);
+        const i32x4 a = *reinterpret_cast<const i32x4*>(sd + kbase + cc * 2048 + kb * 512);
+        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[cc], cc == 0 ? i32x16{} : s[kb], 0, 0, 0);
       }
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (j < 5) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
 
-    const bool full = live == ~0ull;
-    i32x8 pf[QB];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      if (!full) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (!((live >> (h * 32 + kb * 16 + i)) & 1)) s[qb][kb][i] = kDead;
-      }
-      int im = s[qb][0][0];
+    if (live != ~0ull) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) im = max(im, s[qb][kb][i]);
-      im = max(im, other_half_i(im));
-      const float sc = qscale[qb] * ksc;
-      const float tmax = im == kDead ? -__builtin_inff() : float(im) * sc;
-      const float next = fmaxf(m[qb], tmax);
-      const float alpha = m[qb] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m[qb] - next);
-      const float base = next == -__builtin_inff() ? 0.f : kLog2_448 - next;
-      m[qb] = next;
-      float f[32];
-      float ts = 0.f;
+        for (int ii = 0; ii < 16; ++ii)
+          if (!((live >> (h * 32 + kb * 16 + ii)) & 1)) s[kb][ii] = kDead;
+    }
+    int im = s[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int ii = 0; ii < 16; ++ii) im = max(im, s[kb][ii]);
+    im = max(im, other_half_i(im));
+    const float sc = qscale * ksc;
+    const float tmax = im == kDead ? -__builtin_inff() : float(im) * sc;
+    const float mnew = tmax > m + kSageHeadroom ? tmax : m;
+    const float alpha = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+    m = mnew;
+    const float base = mnew == -__builtin_inff() ? 0.f : kLog2_448 - kSageHeadroom - mnew;
+    float f[32];
+    float ts = 0.f;
+    if (live == ~0ull) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int si = s[qb][kb][i];
-          float e = __builtin_amdgcn_exp2f(__builtin_fmaf(float(si), sc, base));
-          if (!full) e = si == kDead ? 0.f : e;
-          f[kb * 16 + i] = e;
+        for (int ii = 0; ii < 16; ++ii) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(float(s[kb][ii]), sc, base));
+          f[kb * 16 + ii] = e;
           ts += e;
         }
-      ts += other_half(ts);
-      l[qb] = l[qb] * alpha + ts;
-      if (!__all(alpha == 1.f)) {
+    } else {  // dead keys contribute exactly 0 (even when sc == 0)
 #pragma unroll
-        for (int db = 0; db < 4; ++db) acc[qb][db] *= alpha;
-      }
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        uint32_t lo = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(f[4 * w], f[4 * w + 1], 0, false));
-        uint32_t both = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(f[4 * w + 2], f[4 * w + 3], int(lo), true));
-        pf[qb][w] = int(both);
-      }
+        for (int ii = 0; ii < 16; ++ii) {
+          const int si = s[kb][ii];
+          const float e = si == kDead ? 0.f : __builtin_amdgcn_exp2f(__builtin_fmaf(float(si), sc, base));
+          f[kb * 16 + ii] = e;
+          ts += e;
+        }
+    }
+    ts += other_half(ts);
+    l = l * alpha + ts;
+    if (!__all(alpha == 1.f)) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+    }
+    i32x8 pf;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const uint32_t lo = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(f[4 * w], f[4 * w + 1], 0, false));
+      pf[w] = __builtin_amdgcn_cvt_pk_fp8_f32(f[4 * w + 2], f[4 * w + 3], int(lo), true);
     }
 
     // ---- O^T += V^T P^T (e4m3 x e4m3 -> fp32) ----
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const i32x4 a0 = *reinterpret_cast<const i32x4*>(vd + voff[db][0]);
-      const i32x4 a1 = *reinterpret_cast<const i32x4*>(vd + voff[db][1]);
+      const i32x4 a0 = *reinterpret_cast<const i32x4*>(sd + vbase0 + db * 2048);
+      const i32x4 a1 = *reinterpret_cast<const i32x4*>(sd + vbase1 + db * 2048);
       const i32x8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, pf, acc[db], 0, 0, 0, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
-        acc[qb][db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, pf[qb], acc[qb][db], 0, 0, 0, 0, 0, 0);
+    for (int j = 0; j < 4; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (j < 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
   };
-  for (int t = 0; t < nt; t += 2) {
-    tile(t, lds0, lds1);
-    if (t + 1 < nt) tile(t + 1, lds1, lds0);
+  for (int t = 0; t < nt; t += NS) {
+    step(t, std::integral_constant<int, 0>{});
+    if (t + 1 < nt) step(t + 1, std::integral_constant<int, 1>{});
+    if constexpr (NS > 2) if (t + 2 < nt) step(t + 2, std::integral_constant<int, 2>{});
+    if constexpr (NS > 3) if (t + 3 < nt) step(t + 3, std::integral_constant<int, 3>{});
   }
 
   // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----
-  const float* vah = va + kvh * D;
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int row = q0 + qb * 32 + n;
-    if (row >= p.Sq) continue;
-    const float inv = l[qb] > 0.f ? 1.f / (448.f * l[qb]) : 0.f;
+  if (row < p.Sq) {
+    const float* vah = va + kvh * D;
+    const float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
     uint16_t* dst = o + int64_t(row) * p.o_stride + head * D + h * 4;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = db * 32 + g * 8 + h * 4;
-        const float* a = reinterpret_cast<const float*>(&acc[qb][db]) + g * 4;
         const f32x4 sv = *reinterpret_cast<const f32x4*>(vah + d);
         uint32_t* d32 = reinterpret_cast<uint32_t*>(dst + db * 32 + g * 8);
-        d32[0] = pack_bf16x2(a[0] * sv[0] * inv, a[1] * sv[1] * inv);
-        d32[1] = pack_bf16x2(a[2] * sv[2] * inv, a[3] * sv[3] * inv);
+        d32[0] = pack_bf16x2(acc[db][g * 4] * sv[0] * inv, acc[db][g * 4 + 1] * sv[1] * inv);
+        d32[1] = pack_bf16x2(acc[db][g * 4 + 2] * sv[2] * inv, acc[db][g * 4 + 3] * sv[3] * inv);
       }
   }
 }
@@ -433,14 +451,13 @@ hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint
 }
 
 hipError_t launch_sage_attend(uint16_t* o, const mx_attn_params& p, const char* ws, hipStream_t s) {
-  constexpr int NW = MXA_SAGE_NW, QB = MXA_SAGE_QB, QT = NW * 32 * QB;
+  constexpr int QT = 256;
   static_assert(kSqPad % QT == 0, "Q padding must cover whole query tiles");
   const mx_sage_layout L = sage_layout(p);
   const int ntq = (p.Sq + QT - 1) / QT;
   const int64_t blocks = int64_t(ntq) * p.Hq;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  const size_t lds = 0;  // static LDS: two 16 KB K/V stages
-  hipLaunchKernelGGL((sage_attn_d128<NW, QB>), dim3(unsigned(blocks)), dim3(NW * 64), lds, s,
+  hipLaunchKernelGGL((sage_attn_d128<MXA_SAGE_NS>), dim3(unsigned(blocks)), dim3(512), 0, s,
                      reinterpret_cast<const int8_t*>(ws + L.qi), reinterpret_cast<const int8_t*>(ws + L.ki),
                      reinterpret_cast<const uint8_t*>(ws + L.vt), reinterpret_cast<const float*>(ws + L.qs),
                      reinterpret_cast<const float*>(ws + L.ks), reinterpret_cast<const float*>(ws + L.va), o, p,

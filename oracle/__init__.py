@@ -56,7 +56,7 @@ def lib():
         L.or_v_quant.argtypes = [_p, _i, _i, _i, _i64, _i64, _p, _p]
         L.or_sage_emulate.restype = None
         L.or_sage_emulate.argtypes = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64,
-                                      _p, _p, _i, _p, _i]
+                                      _p, _p, _i, _p, _i, _f]
         L.or_num_threads.restype = _i
         _lib = L
     return _lib
@@ -130,7 +130,12 @@ def v_quant(v, Skv, Hkv, D, kv_stride, skv_pad, vamax):
     return vt
 
 
-def sage_emulate(qi, ki, vt, qs, ks, vamax, Sq, Skv, Hq, Hkv, D, kv_valid=None, rows=None, threads=0):
+# Lazy-max headroom of the GPU Sage kernel (log2 units); 0 = reference exact-max rule.
+KERNEL_HEADROOM = 2.0
+
+
+def sage_emulate(qi, ki, vt, qs, ks, vamax, Sq, Skv, Hq, Hkv, D, kv_valid=None, rows=None, threads=0,
+                 headroom=0.0):
     qi = _c(qi, np.int8); ki = _c(ki, np.int8); vt = _c(vt, np.uint8)
     qs = _c(qs, np.float32); ks = _c(ks, np.float32); vamax = _c(vamax, np.float32)
     sq_pad = qi.shape[1]; skv_pad = ki.shape[1]
@@ -139,12 +144,12 @@ def sage_emulate(qi, ki, vt, qs, ks, vamax, Sq, Skv, Hq, Hkv, D, kv_valid=None, 
     out = np.zeros((len(rows), Hq, D), np.float32)
     lib().or_sage_emulate(_ptr(qi), _ptr(ki), _ptr(vt), _ptr(qs), _ptr(ks), _ptr(vamax), Sq, Skv,
                           Hq, Hkv, D, sq_pad, skv_pad, _ptr(mask), _ptr(rows), len(rows),
-                          _ptr(out), threads)
+                          _ptr(out), threads, float(headroom))
     return out
 
 
 def sage_reference(q, k, v, Sq, Skv, Hq, Hkv, D, scale=0.0, q_stride=0, kv_stride=0,
-                   kv_valid=None, rows=None, q_group=16, threads=0):
+                   kv_valid=None, rows=None, q_group=16, threads=0, headroom=0.0):
     """Full Sage pipeline on the CPU: prologue (kv_stats, Q/K int8, V e4m3) + emulator.
 
     Returns (out [rows,Hq,D] f32, dict of quantized tensors)."""
@@ -158,7 +163,7 @@ def sage_reference(q, k, v, Sq, Skv, Hq, Hkv, D, scale=0.0, q_stride=0, kv_strid
     qi, qs = quant_rows(q, q_stride, Sq, sq_pad, Hq, D, q_group, None, mult)
     ki, ks = quant_rows(k, kv_stride, Skv, skv_pad, Hkv, D, 64, km, 1.0)
     vt = v_quant(v, Skv, Hkv, D, kv_stride, skv_pad, va)
-    out = sage_emulate(qi, ki, vt, qs, ks, va, Sq, Skv, Hq, Hkv, D, kv_valid, rows, threads)
+    out = sage_emulate(qi, ki, vt, qs, ks, va, Sq, Skv, Hq, Hkv, D, kv_valid, rows, threads, headroom)
     return out, dict(qi=qi, qs=qs, ki=ki, ks=ks, vt=vt, km=km, va=va)
 
 

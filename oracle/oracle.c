@@ -233,8 +233,9 @@ void or_v_quant(const uint16_t* v, int Skv, int Hkv, int D, int64_t kv_stride, i
  *   s = sum_d qi*ki (int32, exact)                                  :286-304
  *   sc = qs[row/16] * ks[tile]                                      :308
  *   im = max over the tile's live keys (integers), next = max(m, im*sc)  :322-327
+ *     (or the lazy rule with headroom H, see below; H = 0 is the reference)
  *   alpha = 2^(m - next) (0 on the first tile)                      :328
- *   f = 2^(fma(s, sc, log2(448) - next)); dead keys -> 0            :331-338
+ *   f = 2^(fma(s, sc, log2(448) - H - next)); dead keys -> 0        :331-338
  *   l = l*alpha + sum f (unquantized f)                             :345
  *   acc = acc*alpha + sum e4m3(f) * e4m3(vt)  (fp32 accumulate)     :352, :374-402
  *   out = acc*vamax[d] * (1/(448*l)), 0 if l == 0                   :405-416
@@ -248,7 +249,7 @@ void or_v_quant(const uint16_t* v, int Skv, int Hkv, int D, int64_t kv_stride, i
 void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, const float* qs,
                      const float* ks, const float* vamax, int Sq, int Skv, int Hq, int Hkv, int D,
                      int64_t sq_pad, int64_t skv_pad, const uint8_t* kv_valid, const int* rows,
-                     int n_rows, float* out, int threads) {
+                     int n_rows, float* out, int threads, float headroom) {
   (void)Sq;
   const int group = Hq / Hkv;
   const float L448 = 8.807354922057604f;
@@ -281,10 +282,14 @@ void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, cons
         if (live) { live_any = 1; if (dot > im) im = dot; }
       }
       if (!live_any) continue;
-      float next = fmaxf(m, (float)im * sc);
+      const float tmax = (float)im * sc;
+      /* headroom 0: next = max(m, tmax), the reference rule (:327). headroom H > 0:
+       * lazy max, m moves only when the tile max exceeds it by more than H, and P
+       * carries 2^-H so it stays <= 448 (this build's kernel uses H = 2). */
+      float next = tmax > m + headroom ? tmax : m;
       float alpha = m == -INFINITY ? 0.f : (float)exp2((double)(m - next));
       m = next;
-      float base = L448 - next, ts = 0.f;
+      float base = L448 - headroom - next, ts = 0.f;
       for (int j = 0; j < 64; ++j) {
         f[j] = s[j] == INT32_MIN ? 0.f : (float)exp2((double)fmaf((float)s[j], sc, base));
         ts += f[j];

