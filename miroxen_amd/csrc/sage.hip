@@ -20,112 +20,128 @@ namespace {
 constexpr int D = 128;
 
 // ---------------- prologue ----------------
-
-// Per (head, 256-token block): partial K sum / Skv and partial V abs-max per
-// channel (reference kv_stats_kernel, attention_fp8.cu:51-62). Partials replace
-// the reference's float atomics so the K mean has one fixed summation order.
-__global__ void __launch_bounds__(D) kv_stats(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                                              mx_attn_params p, int nb, float* __restrict__ part) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int64_t t0 = int64_t(b) * kStatTok;
-  const int64_t t1 = t0 + kStatTok < p.Skv ? t0 + kStatTok : p.Skv;
-  const uint16_t* kp = k + int64_t(h) * D + d;
-  const uint16_t* vp = v + int64_t(h) * D + d;
-  float s = 0.f, am = 0.f;
-  int64_t t = t0;
-  for (; t + 8 <= t1; t += 8) {
-    uint16_t kk[8], vv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      kk[j] = kp[(t + j) * p.kv_stride];
-      vv[j] = vp[(t + j) * p.kv_stride];
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      s += bf2f(kk[j]);
-      am = fmaxf(am, fabsf(bf2f(vv[j])));
-    }
-  }
-  for (; t < t1; ++t) {
-    s += bf2f(kp[t * p.kv_stride]);
-    am = fmaxf(am, fabsf(bf2f(vp[t * p.kv_stride])));
-  }
-  const int64_t idx = (int64_t(h) * nb + b) * D + d;
-  part[idx] = s / float(p.Skv);
-  part[int64_t(p.Hkv) * nb * D + idx] = am;
-}
-
-// kmean = sum of the partials in ascending block order from 0.f; vamax = max.
-__global__ void __launch_bounds__(D) kv_finalize(mx_attn_params p, int nb, const float* __restrict__ part,
-                                                 float* __restrict__ km, float* __restrict__ va) {
-  const int h = blockIdx.x, d = threadIdx.x;
-  const float* ps = part + int64_t(h) * nb * D + d;
-  const float* pa = ps + int64_t(p.Hkv) * nb * D;
-  float s = 0.f, am = 0.f;
-  for (int b = 0; b < nb; ++b) {
-    s += ps[int64_t(b) * D];
-    am = fmaxf(am, pa[int64_t(b) * D]);
-  }
-  km[h * D + d] = s;
-  va[h * D + d] = am;
-}
+//
+// Three launches (the reference uses a memset and four kernels, :433-446):
+//  1. prep_stats_q: blocks [0, Hkv*nb) reduce K/V statistics of one 256-token
+//     block of one head; the remaining blocks quantize Q (one 16-row group per
+//     wave). K/V rows are staged through LDS with 16-byte coalesced loads, then
+//     each channel is summed sequentially over the block's tokens from LDS.
+//  2. prep_finalize: K mean (partials summed in ascending block order from 0.f)
+//     and V abs-max per (head, channel).
+//  3. prep_kv_quant: per (64-key tile, head): K - mean -> INT8 with one scale per
+//     tile, V -> e4m3 transposed to V^T.
+// Arithmetic follows the reference's quant_rows_kernel / kv_stats_kernel /
+// v_quant_kernel (attention_fp8.cu:51-127) operation for operation, so the
+// quantized bytes and scales are bit-identical to the oracle's restatement.
 
 __device__ __forceinline__ float wave_max(float x) {
   for (int off = 32; off; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
   return x;
 }
 
-// Symmetric INT8 quantization of G-token groups of one head
-// (reference quant_rows_kernel, attention_fp8.cu:65-100): x' = bf16(x) - mean,
-// amax over the group, inv = amax>0 ? 127/amax : 0, q = rint(x'*inv),
-// scale = amax/127*mult; rows >= S are zero. 128 threads, 8 channels per load.
-template <int G>
-__global__ void __launch_bounds__(128) quant_rows(const uint16_t* __restrict__ x, int64_t stride, int S,
-                                                  int64_t s_pad, const float* __restrict__ mean, float mult,
-                                                  int8_t* __restrict__ out, float* __restrict__ scale) {
-  constexpr int NV = G * D / 8 / 128;
-  __shared__ float red[2];
-  const int h = blockIdx.y, grp = blockIdx.x;
-  float vals[NV][8], am = 0.f;
+// Symmetric INT8 of 8 floats with a shared inverse scale (reference :96).
+__device__ __forceinline__ u32x2 quant8(const float (&x)[8], float inv) {
+  u32x2 w = {0, 0};
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int vi = threadIdx.x + i * 128, r = vi / (D / 8), c = (vi % (D / 8)) * 8;
-    const int64_t row = int64_t(grp) * G + r;
+  for (int j = 0; j < 8; ++j) w[j >> 2] |= uint32_t(int(__builtin_rintf(x[j] * inv)) & 0xff) << ((j & 3) * 8);
+  return w;
+}
+
+constexpr int kStatChunk = 128;  // tokens staged in LDS per step of a stats block
+
+__global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                    const uint16_t* __restrict__ v, mx_attn_params p, int nb,
+                                                    float qmult, int64_t sq_pad, float* __restrict__ part,
+                                                    int8_t* __restrict__ qi, float* __restrict__ qs) {
+  __shared__ __align__(16) uint16_t kt[kStatChunk * D];
+  __shared__ __align__(16) uint16_t vt_[kStatChunk * D];
+  const int tid = threadIdx.x, nstat = p.Hkv * nb;
+  if (int(blockIdx.x) < nstat) {
+    // ---- K sum / V abs-max over tokens [b*256, min(b*256+256, Skv)) of head h ----
+    const int h = blockIdx.x / nb, b = blockIdx.x % nb;
+    const int64_t t0 = int64_t(b) * kStatTok;
+    const int64_t t1 = t0 + kStatTok < p.Skv ? t0 + kStatTok : p.Skv;
+    float sum = 0.f, am = 0.f;
+    for (int64_t c0 = t0; c0 < t1; c0 += kStatChunk) {
+      const int rows = int(t1 - c0 < kStatChunk ? t1 - c0 : kStatChunk);
+      for (int i = tid; i < rows * (D / 8); i += 256) {
+        const int r = i / (D / 8), c = (i % (D / 8)) * 8;
+        const int64_t g = (c0 + r) * p.kv_stride + int64_t(h) * D + c;
+        *reinterpret_cast<u32x4*>(&kt[r * D + c]) = *reinterpret_cast<const u32x4*>(k + g);
+        *reinterpret_cast<u32x4*>(&vt_[r * D + c]) = *reinterpret_cast<const u32x4*>(v + g);
+      }
+      __syncthreads();
+      if (tid < D) {
+#pragma unroll 16
+        for (int r = 0; r < rows; ++r) sum += bf2f(kt[r * D + tid]);  // sequential, token order
+      } else {
+        const int d = tid - D;
+#pragma unroll 16
+        for (int r = 0; r < rows; ++r) am = fmaxf(am, fabsf(bf2f(vt_[r * D + d])));
+      }
+      __syncthreads();
+    }
+    if (tid < D) part[(int64_t(h) * nb + b) * D + tid] = sum / float(p.Skv);
+    else part[int64_t(p.Hkv) * nb * D + (int64_t(h) * nb + b) * D + (tid - D)] = am;
+    return;
+  }
+  // ---- Q: one 16-row group per wave; lane owns 4 chunks of 8 channels ----
+  const int wave = tid >> 6, lane = tid & 63;
+  const int64_t gid = (int64_t(blockIdx.x) - nstat) * 4 + wave;  // group index over (head, group)
+  const int ng = int(sq_pad / 16);
+  if (gid >= int64_t(p.Hq) * ng) return;
+  const int h = int(gid / ng), grp = int(gid % ng);
+  float x[4][8], am = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ci = lane + i * 64, r = ci >> 4, c = (ci & 15) * 8;
+    const int64_t row = int64_t(grp) * 16 + r;
     u32x4 raw = {0, 0, 0, 0};
-    if (row < S) raw = *reinterpret_cast<const u32x4*>(x + row * stride + int64_t(h) * D + c);
+    if (row < p.Sq) raw = *reinterpret_cast<const u32x4*>(q + row * p.q_stride + int64_t(h) * D + c);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const uint16_t bits = uint16_t(raw[j >> 1] >> ((j & 1) * 16));
-      float f = 0.f;
-      if (row < S) {
-        f = bf2f(bits);
-        if (mean) f = f - mean[h * D + c + j];
-      }
-      vals[i][j] = f;
-      am = fmaxf(am, fabsf(f));
+      x[i][j] = bf2f(uint16_t(raw[j >> 1] >> ((j & 1) * 16)));
+      am = fmaxf(am, fabsf(x[i][j]));
     }
   }
   am = wave_max(am);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
-  __syncthreads();
-  am = fmaxf(red[0], red[1]);
   const float inv = am > 0.f ? 127.f / am : 0.f;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int vi = threadIdx.x + i * 128, r = vi / (D / 8), c = (vi % (D / 8)) * 8;
-    u32x2 w = {0, 0};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int qv = int(__builtin_rintf(vals[i][j] * inv));
-      w[j >> 2] |= uint32_t(qv & 0xff) << ((j & 3) * 8);
-    }
-    *reinterpret_cast<u32x2*>(out + (int64_t(h) * s_pad + int64_t(grp) * G + r) * D + c) = w;
+  for (int i = 0; i < 4; ++i) {
+    const int ci = lane + i * 64, r = ci >> 4, c = (ci & 15) * 8;
+    *reinterpret_cast<u32x2*>(qi + (int64_t(h) * sq_pad + int64_t(grp) * 16 + r) * D + c) = quant8(x[i], inv);
   }
-  if (threadIdx.x == 0) scale[int64_t(h) * (s_pad / G) + grp] = am / 127.f * mult;
+  if (lane == 0) qs[int64_t(h) * (sq_pad / 16) + grp] = am / 127.f * qmult;
+}
+
+// kmean = sum of the partials in ascending block order from 0.f; vamax = max.
+__global__ void __launch_bounds__(D) prep_finalize(mx_attn_params p, int nb, const float* __restrict__ part,
+                                                   float* __restrict__ km, float* __restrict__ va) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  const float* ps = part + int64_t(h) * nb * D + d;
+  const float* pa = ps + int64_t(p.Hkv) * nb * D;
+  float s = 0.f, am = 0.f;
+  constexpr int B = 16;
+  for (int b0 = 0; b0 < nb; b0 += B) {
+    float xs[B], xa[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j) {  // issue the batch's loads before summing
+      xs[j] = b0 + j < nb ? ps[int64_t(b0 + j) * D] : 0.f;
+      xa[j] = b0 + j < nb ? pa[int64_t(b0 + j) * D] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      if (b0 + j < nb) {
+        s += xs[j];
+        am = fmaxf(am, xa[j]);
+      }
+  }
+  km[h * D + d] = s;
+  va[h * D + d] = am;
 }
 
 // OCP e4m3 of two floats (round to nearest even), saturated to +/-448 first
-// (v_cvt_pk_fp8_f32 itself returns NaN above 464, the reference's conversion
+// (v_cvt_pk_fp8_f32 itself returns NaN above 464; the reference's conversion
 // saturates: __NV_SATFINITE at attention_fp8.cu:119).
 __device__ __forceinline__ uint32_t e4m3x2_sat(float a, float b) {
   a = __builtin_fminf(__builtin_fmaxf(a, -448.f), 448.f);
@@ -133,36 +149,75 @@ __device__ __forceinline__ uint32_t e4m3x2_sat(float a, float b) {
   return uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false)) & 0xffffu;
 }
 
-// V -> e4m3 with per-channel scale 448/amax, transposed to [H][D][skv_pad]
-// in natural key order (reference v_quant_kernel, attention_fp8.cu:110-127).
-// One work-group per (64-key tile, head); 256 threads.
-__global__ void __launch_bounds__(256) v_quant(const uint16_t* __restrict__ v, mx_attn_params p, int64_t skv_pad,
-                                               const float* __restrict__ va, uint8_t* __restrict__ vt) {
-  __shared__ __align__(16) uint8_t tile[D][kKvPad + 4];
-  const int h = blockIdx.y, k0 = blockIdx.x * kKvPad;
-  // each thread converts 8 channels of 4 keys: 64 keys x 16 chunks = 1024 chunks / 256 threads
-  for (int i = threadIdx.x; i < kKvPad * (D / 8); i += 256) {
-    const int key = i / (D / 8), c = (i % (D / 8)) * 8;
-    const int64_t gk = k0 + key;
-    u32x4 raw = {0, 0, 0, 0};
-    if (gk < p.Skv) raw = *reinterpret_cast<const u32x4*>(v + gk * p.kv_stride + int64_t(h) * D + c);
+// Per (64-key tile, head): K - mean -> INT8 (one scale per tile) and V -> e4m3
+// transposed to [H][D][skv_pad] in natural key order. Thread tid owns channel
+// chunk tid%16 (8 channels) of rows tid/16 + 16*i, i = 0..3.
+__global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                                     mx_attn_params p, int64_t skv_pad,
+                                                     const float* __restrict__ km, const float* __restrict__ va,
+                                                     int8_t* __restrict__ ki, float* __restrict__ ks,
+                                                     uint8_t* __restrict__ vt) {
+  __shared__ __align__(16) uint8_t tile[D][kKvPad + 16];
+  __shared__ float red[4];
+  const int h = blockIdx.y, k0 = blockIdx.x * kKvPad, tid = threadIdx.x;
+  const int c = (tid & 15) * 8, r0 = tid >> 4;
+  float mean[8], vsc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    mean[j] = km[h * D + c + j];
+    const float a = va[h * D + c + j];
+    vsc[j] = a > 0.f ? 448.f / a : 0.f;
+  }
+  u32x4 kraw[4], vraw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = k0 + r0 + 16 * i;
+    kraw[i] = vraw[i] = u32x4{0, 0, 0, 0};
+    if (row < p.Skv) {
+      const int64_t g = row * p.kv_stride + int64_t(h) * D + c;
+      kraw[i] = *reinterpret_cast<const u32x4*>(k + g);
+      vraw[i] = *reinterpret_cast<const u32x4*>(v + g);
+    }
+  }
+  // K: x' = bf16(x) - mean (rows >= Skv are 0), amax over the tile
+  float x[4][8], am = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool ok = k0 + r0 + 16 * i < p.Skv;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      x[i][j] = ok ? bf2f(uint16_t(kraw[i][j >> 1] >> ((j & 1) * 16))) - mean[j] : 0.f;
+      am = fmaxf(am, fabsf(x[i][j]));
+    }
+  }
+  // V -> e4m3 into the transposed LDS tile while the K amax reduces
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = r0 + 16 * i;
+    const bool ok = k0 + key < p.Skv;
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
-      const float a0 = va[h * D + c + j], a1 = va[h * D + c + j + 1];
-      const float f0 = gk < p.Skv && a0 > 0.f ? bf2f(uint16_t(raw[j >> 1])) * (448.f / a0) : 0.f;
-      const float f1 = gk < p.Skv && a1 > 0.f ? bf2f(uint16_t(raw[j >> 1] >> 16)) * (448.f / a1) : 0.f;
+      const float f0 = ok && vsc[j] > 0.f ? bf2f(uint16_t(vraw[i][j >> 1])) * vsc[j] : 0.f;
+      const float f1 = ok && vsc[j + 1] > 0.f ? bf2f(uint16_t(vraw[i][j >> 1] >> 16)) * vsc[j + 1] : 0.f;
       const uint32_t pk = e4m3x2_sat(f0, f1);
       tile[c + j][key] = uint8_t(pk);
       tile[c + j + 1][key] = uint8_t(pk >> 8);
     }
   }
+  am = wave_max(am);
+  if ((tid & 63) == 0) red[tid >> 6] = am;
   __syncthreads();
-  for (int i = threadIdx.x; i < D * (kKvPad / 16); i += 256) {
-    const int d = i / (kKvPad / 16), u = i % (kKvPad / 16);
-    u32x4 w;
+  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float inv = am > 0.f ? 127.f / am : 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const uint32_t*>(&tile[d][u * 16 + 4 * j]);
-    *reinterpret_cast<u32x4*>(vt + (int64_t(h) * D + d) * skv_pad + k0 + u * 16) = w;
+  for (int i = 0; i < 4; ++i)
+    *reinterpret_cast<u32x2*>(ki + (int64_t(h) * skv_pad + k0 + r0 + 16 * i) * D + c) = quant8(x[i], inv);
+  if (tid == 0) ks[int64_t(h) * (skv_pad / kKvPad) + blockIdx.x] = am / 127.f * 1.f;
+  // V^T rows: channel d, 64 keys = 4 x 16 bytes
+  for (int i = tid; i < D * (kKvPad / 16); i += 256) {
+    const int d = i / (kKvPad / 16), u = i % (kKvPad / 16);
+    *reinterpret_cast<u32x4*>(vt + (int64_t(h) * D + d) * skv_pad + k0 + u * 16) =
+        *reinterpret_cast<const u32x4*>(&tile[d][u * 16]);
   }
 }
 
@@ -436,17 +491,16 @@ hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint
   float* part = reinterpret_cast<float*>(ws + L.part);
   float* km = reinterpret_cast<float*>(ws + L.km);
   float* va = reinterpret_cast<float*>(ws + L.va);
-  hipLaunchKernelGGL(kv_stats, dim3(p.Hkv, nb), dim3(D), 0, s, k, v, p, nb, part);
-  hipLaunchKernelGGL(kv_finalize, dim3(p.Hkv), dim3(D), 0, s, p, nb, part, km, va);
+  const int64_t qgroups = int64_t(p.Hq) * (L.sq_pad / 16);
+  const int64_t blocks1 = int64_t(p.Hkv) * nb + (qgroups + 3) / 4;
+  if (blocks1 > 0x7fffffff) return hipErrorInvalidValue;
   const float qmult = p.scale * kLog2e;
-  hipLaunchKernelGGL(quant_rows<16>, dim3(unsigned(L.sq_pad / 16), p.Hq), dim3(128), 0, s, q, p.q_stride, p.Sq,
-                     L.sq_pad, (const float*)nullptr, qmult, reinterpret_cast<int8_t*>(ws + L.qi),
-                     reinterpret_cast<float*>(ws + L.qs));
-  hipLaunchKernelGGL(quant_rows<kKvPad>, dim3(unsigned(L.skv_pad / kKvPad), p.Hkv), dim3(128), 0, s, k, p.kv_stride,
-                     p.Skv, L.skv_pad, (const float*)km, 1.f, reinterpret_cast<int8_t*>(ws + L.ki),
-                     reinterpret_cast<float*>(ws + L.ks));
-  hipLaunchKernelGGL(v_quant, dim3(unsigned(L.skv_pad / kKvPad), p.Hkv), dim3(256), 0, s, v, p, L.skv_pad,
-                     (const float*)va, reinterpret_cast<uint8_t*>(ws + L.vt));
+  hipLaunchKernelGGL(prep_stats_q, dim3(unsigned(blocks1)), dim3(256), 0, s, q, k, v, p, nb, qmult, L.sq_pad, part,
+                     reinterpret_cast<int8_t*>(ws + L.qi), reinterpret_cast<float*>(ws + L.qs));
+  hipLaunchKernelGGL(prep_finalize, dim3(p.Hkv), dim3(D), 0, s, p, nb, (const float*)part, km, va);
+  hipLaunchKernelGGL(prep_kv_quant, dim3(unsigned(L.skv_pad / kKvPad), p.Hkv), dim3(256), 0, s, k, v, p, L.skv_pad,
+                     (const float*)km, (const float*)va, reinterpret_cast<int8_t*>(ws + L.ki),
+                     reinterpret_cast<float*>(ws + L.ks), reinterpret_cast<uint8_t*>(ws + L.vt));
   return hipGetLastError();
 }
 
