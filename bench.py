@@ -129,6 +129,9 @@ def main() -> int:
         "prologue_ms": round(ms_pro, 4), "prologue_gbs": round(pro_bytes / (ms_pro * 1e-3) / 1e9, 1),
         "prologue_frac_hbm": round(pro_bytes / (ms_pro * 1e-3) / 1e9 / PEAK_HBM, 4),
         "dtype": "int8 QK^T / e4m3 PV, fp32 accumulate",
+        "roofline": {"bound": "mfma", "achieved": round(flop / (ms_main * 1e-3) / 1e12, 2), "peak": PEAK_FP8,
+                     "unit": "TFLOP/s", "frac": round(flop / (ms_main * 1e-3) / 1e12 / PEAK_FP8, 4),
+                     "traffic": _traffic("sage_attn_config3")},
     }
 
     traffic = _traffic("flash_bf16_config2")

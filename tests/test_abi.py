@@ -94,3 +94,18 @@ def test_workspace_and_layout():
     order = [L2[n] for n in ("qi", "ki", "vt", "qs", "ks", "km", "va", "part", "total")]
     assert order == sorted(order)
     assert L2["ki"] - L2["qi"] >= 4 * 1024 * 128 and L2["vt"] - L2["ki"] >= 2 * 128 * 128
+
+
+def test_cpp_dropin_header_rejects_invalid_inputs(tmp_path):
+    """Compile the reference-style invalid-input test against include/miroxen/attention.h
+    and libmiroxen_attn.so, and run it (host-side validation only, no GPU needed)."""
+    import subprocess
+    exe = tmp_path / "invalid_inputs"
+    lib_dir = os.path.dirname(_lib.LIB_PATH)
+    cmd = ["/opt/rocm/bin/hipcc", "-std=c++17", "-O1", "-I", os.path.join(ROOT, "include"),
+           os.path.join(ROOT, "tests", "cpp", "invalid_inputs.cpp"), "-L", lib_dir, "-lmiroxen_attn",
+           f"-Wl,-rpath,{lib_dir}", "-o", str(exe)]
+    subprocess.run(cmd, check=True, capture_output=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "23 rejected" in r.stdout
