@@ -247,6 +247,10 @@ constexpr int KTILEB = KT * D;        // 8 KB int8 K tile
 constexpr int VTILEB = D * KT;        // 8 KB fp8 V^T tile
 constexpr int STAGEB = KTILEB + VTILEB;
 constexpr float kSageHeadroom = 2.f;
+constexpr int kScoreBias = 0x4B400000;  // bits of 12582912.0f = 1.5 * 2^23
+constexpr i32x16 kScoreBias16 = {kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
+                                 kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
+                                 kScoreBias, kScoreBias, kScoreBias, kScoreBias};
 #ifndef MXA_SAGE_NS
 #define MXA_SAGE_NS 2
 #endif
@@ -353,7 +357,9 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const i32x4 a = *reinterpret_cast<const i32x4*>(sd + kbase + cc * 2048 + kb * 512);
-        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[cc], cc == 0 ? i32x16{} : s[kb], 0, 0, 0);
+        // accumulate on top of the bias 0x4B400000: the float with those bits + s is
+        // exactly 12582912 + s (|s| < 2^22), so no int->float conversion is needed
+        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[cc], cc == 0 ? kScoreBias16 : s[kb], 0, 0, 0);
       }
     __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
 #pragma unroll
@@ -376,44 +382,41 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
       for (int ii = 0; ii < 16; ++ii) im = max(im, s[kb][ii]);
     im = max(im, other_half_i(im));
     const float sc = qscale * ksc;
-    const float tmax = im == kDead ? -__builtin_inff() : float(im) * sc;
+    const float tmax = im == kDead ? -__builtin_inff() : float(im - kScoreBias) * sc;
     const float mnew = tmax > m + kSageHeadroom ? tmax : m;
     const float alpha = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
     m = mnew;
-    const float base = mnew == -__builtin_inff() ? 0.f : kLog2_448 - kSageHeadroom - mnew;
-    float f[32];
+    // exponent = (12582912 + s)*sc + nm with nm = (log2 448 - H - m) - 12582912*sc
+    // (reference attention_fp8.cu:331, :337, plus the headroom H)
+    const float nm =
+        mnew == -__builtin_inff() ? -__builtin_inff() : (kLog2_448 - kSageHeadroom - mnew) - 12582912.f * sc;
+    // P = 2^exponent packed to e4m3 four at a time: byte j of the 32-byte B operand
+    // is key 32h + j (j = kb*16 + ii); l sums the unquantized values
     float ts = 0.f;
-    if (live == ~0ull) {
+    i32x8 pf;
+    auto pexp = [&](int si, auto masked) __attribute__((always_inline)) -> float {
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(__int_as_float(si), sc, nm));
+      if constexpr (decltype(masked)::value) return si == kDead ? 0.f : e;
+      return e;
+    };
+    auto pack = [&](auto masked) __attribute__((always_inline)) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int ii = 0; ii < 16; ++ii) {
-          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(float(s[kb][ii]), sc, base));
-          f[kb * 16 + ii] = e;
-          ts += e;
-        }
-    } else {  // dead keys contribute exactly 0 (even when sc == 0)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int ii = 0; ii < 16; ++ii) {
-          const int si = s[kb][ii];
-          const float e = si == kDead ? 0.f : __builtin_amdgcn_exp2f(__builtin_fmaf(float(si), sc, base));
-          f[kb * 16 + ii] = e;
-          ts += e;
-        }
-    }
+      for (int w = 0; w < 8; ++w) {
+        const int kb = w >> 2, i0 = (w & 3) * 4;
+        const float e0 = pexp(s[kb][i0], masked), e1 = pexp(s[kb][i0 + 1], masked);
+        const float e2 = pexp(s[kb][i0 + 2], masked), e3 = pexp(s[kb][i0 + 3], masked);
+        ts += (e0 + e1) + (e2 + e3);
+        const uint32_t lo = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(e0, e1, 0, false));
+        pf[w] = __builtin_amdgcn_cvt_pk_fp8_f32(e2, e3, int(lo), true);
+      }
+    };
+    if (live == ~0ull) pack(std::false_type{});
+    else pack(std::true_type{});  // dead keys contribute exactly 0 (even when sc == 0)
     ts += other_half(ts);
     l = l * alpha + ts;
     if (!__all(alpha == 1.f)) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-    }
-    i32x8 pf;
-#pragma unroll
-    for (int w = 0; w < 8; ++w) {
-      const uint32_t lo = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(f[4 * w], f[4 * w + 1], 0, false));
-      pf[w] = __builtin_amdgcn_cvt_pk_fp8_f32(f[4 * w + 2], f[4 * w + 3], int(lo), true);
     }
 
     // ---- O^T += V^T P^T (e4m3 x e4m3 -> fp32) ----

@@ -235,15 +235,15 @@ void or_v_quant(const uint16_t* v, int Skv, int Hkv, int D, int64_t kv_stride, i
  *   im = max over the tile's live keys (integers), next = max(m, im*sc)  :322-327
  *     (or the lazy rule with headroom H, see below; H = 0 is the reference)
  *   alpha = 2^(m - next) (0 on the first tile)                      :328
- *   f = 2^(fma(s, sc, log2(448) - H - next)); dead keys -> 0        :331-338
+ *   f = 2^(fma(bits(s + 0x4B400000), sc, nm)), nm = (log2 448 - H - next)
+ *       - 12582912*sc; dead keys -> 0                                  :331-338
  *   l = l*alpha + sum f (unquantized f)                             :345
  *   acc = acc*alpha + sum e4m3(f) * e4m3(vt)  (fp32 accumulate)     :352, :374-402
  *   out = acc*vamax[d] * (1/(448*l)), 0 if l == 0                   :405-416
  * "Dead" keys are keys >= Skv (the reference's tail, :309-316) and keys with
  * kv_valid[key] == 0 (the build's key-padding mask). A tile with no live key for
- * a row leaves m, l and acc unchanged. The exponent uses an fma of the exact
- * int->float score instead of the reference's bit-trick sum (:331, :337): same
- * value up to one fp32 rounding, which no reference test resolves.
+ * a row leaves m, l and acc unchanged. The exponent follows the reference's
+ * bit-trick formulation operation for operation (:331, :337).
  * exp2 here is libm's double exp2 rounded to float (the GPU uses v_exp_f32,
  * < 1 ulp). out: [n_rows][Hq][D] f32 (before the bf16 store). */
 void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, const float* qs,
@@ -289,9 +289,17 @@ void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, cons
       float next = tmax > m + headroom ? tmax : m;
       float alpha = m == -INFINITY ? 0.f : (float)exp2((double)(m - next));
       m = next;
-      float base = L448 - headroom - next, ts = 0.f;
+      /* exponent as the reference computes it (:331, :337): the int32 score is read as
+       * the float 12582912 + s through its bits (s + 0x4B400000), one FMA with
+       * nm = (log2 448 - H - next) - 12582912*sc (two float roundings). */
+      const float nm = (L448 - headroom - next) - 12582912.f * sc;
+      float ts = 0.f;
       for (int j = 0; j < 64; ++j) {
-        f[j] = s[j] == INT32_MIN ? 0.f : (float)exp2((double)fmaf((float)s[j], sc, base));
+        if (s[j] == INT32_MIN) { f[j] = 0.f; continue; }
+        int32_t biased = s[j] + 0x4B400000;
+        float sb;
+        memcpy(&sb, &biased, 4);
+        f[j] = (float)exp2((double)fmaf(sb, sc, nm));
         ts += f[j];
       }
       l = l * alpha + ts;

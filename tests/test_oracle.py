@@ -242,9 +242,10 @@ def test_sage_single_live_key_returns_dequantized_v():
     q = _bf16_rand(rng, (Sq, H, D)); k = _bf16_rand(rng, (Skv, H, D)); v = _bf16_rand(rng, (Skv, H, D))
     mask = np.zeros(Skv, np.uint8); mask[37] = 1
     out, t = oracle.sage_reference(q, k, v, Sq, Skv, H, H, D, kv_valid=mask)
-    # one live key: P = 448 exactly, l = 448 -> out = e4m3(v*448/a) * a / 448
+    # one live key: P = e4m3(~448) = 448, l ~ 448 (up to the exponent's float rounding in
+    # the reference formulation) -> out = e4m3(v*448/a) * a / 448
     deq = np.array([oracle.e4m3_to_f32(c) for c in t["vt"][0, :, 37]], np.float32) * t["va"][0] / np.float32(448)
-    np.testing.assert_allclose(out[:, 0, :], np.broadcast_to(deq, (Sq, D)), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(out[:, 0, :], np.broadcast_to(deq, (Sq, D)), rtol=1e-4, atol=1e-7)
 
 
 def test_sage_uniform_scores_give_mean_of_dequantized_v():
