@@ -26,13 +26,19 @@ PEAK_FP8 = 5000.0      # TFLOP/s, dense FP8 (INT8 5.0 POP/s)
 PEAK_HBM = 8000.0      # GB/s
 
 
-def _time(fn, steps: int, warmup: int) -> float:
+def _time(fn, steps: int, warmup: int, warm_s: float) -> float:
     """Average ms per call over `steps` calls, HIP events on the stream the kernels use
-    (torch's current stream: the library launches on it)."""
+    (torch's current stream: the library launches on it). Warm-up: `warmup` calls and
+    at least `warm_s` seconds of back-to-back calls, so the timed calls run at the
+    GPU's sustained clock (it needs tens of ms of load to leave its idle clock state)."""
     import torch
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < warm_s:
+        for _ in range(8):
+            fn()
+        n += 8
+        torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
@@ -81,8 +87,10 @@ def cpu_baseline(q, k, v, mask, S, H, D, budget_s: float = 12.0):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warm-seconds", type=float, default=0.5,
+                    help="minimum seconds of untimed back-to-back calls before each timed region")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -106,7 +114,7 @@ def main() -> int:
     eff_flop = attn_flops(H, S, int(mask.sum()), D)
 
     t0 = time.perf_counter()
-    ms = _time(lambda: flash_attn(q, k, v, o, p), args.steps, args.warmup)
+    ms = _time(lambda: flash_attn(q, k, v, o, p), args.steps, args.warmup, args.warm_seconds)
     wall = time.perf_counter() - t0
     tflops = flop / (ms * 1e-3) / 1e12
 
@@ -116,9 +124,9 @@ def main() -> int:
     p3 = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=D, kv_valid=m3)
     ws = torch.empty(flash_attn_fp8_workspace(p3), dtype=torch.uint8, device=dev)
     o3 = torch.empty_like(q3)
-    ms_e2e = _time(lambda: flash_attn_fp8(q3, k3, v3, o3, p3, ws), args.steps, args.warmup)
-    ms_pro = _time(lambda: sage_quantize(q3, k3, v3, p3, ws), args.steps, args.warmup)
-    ms_main = _time(lambda: sage_attend(o3, p3, ws), args.steps, args.warmup)
+    ms_e2e = _time(lambda: flash_attn_fp8(q3, k3, v3, o3, p3, ws), args.steps, args.warmup, args.warm_seconds)
+    ms_pro = _time(lambda: sage_quantize(q3, k3, v3, p3, ws), args.steps, args.warmup, args.warm_seconds)
+    ms_main = _time(lambda: sage_attend(o3, p3, ws), args.steps, args.warmup, args.warm_seconds)
     pro_bytes = 9.0 * S * H * D  # read Q,K,V bf16 + write int8 Q, int8 K, fp8 V
     sage = {
         "workload": c3.name, "ms_end_to_end": round(ms_e2e, 4),

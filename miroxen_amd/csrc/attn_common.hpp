@@ -1,6 +1,9 @@
 // Shared device/host helpers for the gfx950 attention kernels.
 #pragma once
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
+#include <utility>
 #include <stdint.h>
 
 #include "miroxen_attn.h"
@@ -50,6 +53,30 @@ __device__ __forceinline__ int other_half_i(int x) {
 // 16-byte global -> LDS copy: lane i of the wave writes lds_wave_base + 16*i.
 __device__ __forceinline__ void g2lds16(const void* g, MXA_LDS void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(g, lds_wave_base, 16, 0, 0);
+}
+
+// f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N-1>{}).
+template <typename F, int... J>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, J...>) {
+  (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Raw buffer resource over `bytes` bytes from `base` (gfx9 dword3: 32-bit data,
+// no swizzle). Loads at offsets >= bytes return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+
+// 16 bytes per lane from rsrc + voff + soff into LDS at lds_wave_base + 16 * lane.
+// Constant offsets go in soff: an instruction offset would also move the LDS
+// destination of a buffer-to-LDS load.
+__device__ __forceinline__ void buf2lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                          MXA_LDS void* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_wave_base, 16, voff, soff, 0, 0);
 }
 
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }

@@ -14,27 +14,30 @@
 //  * O^T = V^T * P^T with the same MFMA; the V^T operand comes straight from the
 //    row-major V tile with ds_read_b64_tr_b16 (gfx950 transposing LDS read).
 //  * K and V tiles (64 keys) are double-buffered in LDS, filled by
-//    global_load_lds_dwordx4 (16 B per lane, no VGPR staging) one tile ahead, in
-//    bank-conflict-free layouts whose read addresses are one per-lane register
-//    plus compile-time offsets (no per-chunk address registers). The buffers are
+//    buffer_load_dwordx4 ... lds (16 B per lane, no VGPR staging) through a
+//    per-tile buffer resource, in bank-conflict-free layouts whose read addresses
+//    are one per-lane register plus compile-time offsets. The buffers are
 //    distinct LDS objects and the tile loop is unrolled twice, so the compiler can
 //    prove an in-flight DMA never aliases the buffers being read and does not
-//    wait for it; waits are explicit, counted vmcnt.
-//  * Two work-group shapes (selected at build time, MXA_BF16_KIND):
-//     W8 (default): 8 waves of 32 queries, two waves per SIMD; per tile
-//        S -> softmax -> P*V, the other wave on the SIMD fills MFMA gaps.
-//     W4S: 4 waves of 2x32 queries (blocks A, B), one wave per SIMD, the blocks
-//        staggered half a tile so each MFMA phase has independent softmax work:
-//        S_A(t) || softmax_B(t-1); P_B V(t-1) || softmax_A(t); S_B(t); P_A V(t).
-//    Within a phase, sched_group_barrier keeps LDS operand reads a few MFMAs
-//    ahead of use and spreads the VALU work between MFMAs.
+//    wait for it; waits are explicit, counted vmcnt. DMA ops are spread one per
+//    four MFMAs (a burst of them stalls the issuing waves for hundreds of cycles).
+//  * Two work-group shapes (selected at build time, MXA_BF16_KIND), both
+//    8 waves of 32 queries, two waves per SIMD:
+//     PP (9, default): ping-pong. The two waves of a SIMD run the same program
+//        one period apart, so one issues the tile's MFMAs while the other runs
+//        the softmax (VALU); measured ~5% faster than W8.
+//     W8 (8): lockstep, per tile S -> softmax -> P*V on every wave.
+//    Within an MFMA phase, sched_group_barrier keeps LDS operand reads a few
+//    MFMAs ahead of use.
 //  * Work-groups are remapped so one head's query tiles share an XCD (and its L2).
 #include <type_traits>
+#include <utility>
+#include <utility>
 
 #include "attn_common.hpp"
 
 #ifndef MXA_BF16_KIND
-#define MXA_BF16_KIND 8
+#define MXA_BF16_KIND 9
 #endif
 #ifndef MXA_KPF
 #define MXA_KPF 3
@@ -42,11 +45,26 @@
 #ifndef MXA_VPF
 #define MXA_VPF 2
 #endif
-#ifndef MXA_SVALU
-#define MXA_SVALU 12
-#endif
 
 namespace mxa {
+
+#ifdef MXA_CLOCK
+// Development hook (off in normal builds): per-work-group shader-clock and
+// real-time durations, written where mx_debug_timing points.
+__device__ uint64_t* g_timing = nullptr;
+extern "C" int mx_debug_timing(void* buf) {
+  return hipMemcpyToSymbol(HIP_SYMBOL(g_timing), &buf, sizeof(buf)) == hipSuccess ? 0 : -2;
+}
+#define MXA_CLOCK_BEGIN const uint64_t clk0_ = __builtin_amdgcn_s_memtime(), rt0_ = __builtin_amdgcn_s_memrealtime();
+#define MXA_CLOCK_END                                                               \
+  if (threadIdx.x == 0 && g_timing) {                                               \
+    g_timing[blockIdx.x * 2] = __builtin_amdgcn_s_memtime() - clk0_;                \
+    g_timing[blockIdx.x * 2 + 1] = __builtin_amdgcn_s_memrealtime() - rt0_;         \
+  }
+#else
+#define MXA_CLOCK_BEGIN
+#define MXA_CLOCK_END
+#endif
 
 namespace {
 
@@ -113,37 +131,46 @@ __device__ __forceinline__ void qblock_init(QBlock& X, const uint16_t* q, const 
   X.alpha = 1.f;
 }
 
-// DMA of one 64-key K or V tile: op j writes 1 KB (64 lanes x 16 B); a wave
-// issues NLD ops, ops j = jj*NW + wave.
+// DMA of one 64-key K or V tile: op j writes 1 KB (64 lanes x 16 B) of the LDS
+// layout above; a wave issues 16/NW ops, j = jj*NW + wave. The global side is a
+// per-tile buffer resource starting at key t*64 of this KV head: rows at or past
+// Skv fall outside it and load as zeros (no clamping), the per-lane part is a
+// loop-invariant byte offset and the per-op part is wave-uniform, so an op costs
+// no vector ALU work. Requires Skv * kv_stride * 2 < 2^32 and a wave-uniform
+// `wave`.
+struct TileAddr {
+  uint32_t lk, lv;  // per-lane byte offsets of this wave's K and V ops
+};
+template <int NW>
+__device__ __forceinline__ TileAddr tile_addr(const mx_attn_params& p, int wave, int lane) {
+  const uint32_t kvs = uint32_t(p.kv_stride);
+  TileAddr a;
+  // K op j = jj*NW + wave: row (j&1)*32 + lane/2 (j&1 == wave&1), 16-byte half
+  // ((lane&1) ^ row bit 3) of d-chunk j/2
+  const uint32_t krow = uint32_t((wave & 1) * 32 + (lane >> 1));
+  a.lk = (krow * kvs + uint32_t(((lane & 1) ^ ((lane >> 4) & 1)) << 3)) * 2u;
+  // V op j: row (j&3)*16 + lane/4 (j&3 == wave&3), 16-byte chunk lane&3 of d-block j/4
+  const uint32_t vrow = uint32_t((wave & 3) * 16 + (lane >> 2));
+  a.lv = (vrow * kvs + uint32_t((lane & 3) * 8)) * 2u;
+  return a;
+}
 template <int NW, bool IS_V>
 __device__ __forceinline__ void load_tile(const uint16_t* src, int t, unsigned char* dst, const mx_attn_params& p,
-                                          int64_t kvbase, int wave, int lane) {
+                                          int64_t kvbase, int wave, const TileAddr& ta) {
   constexpr int NLD = 16 / NW;
   const int key0 = t * KT;
-#pragma unroll
-  for (int jj = 0; jj < NLD; ++jj) {
-    const int j = jj * NW + wave;
-    int row, col;
-    if constexpr (IS_V) {  // d-block j/4, rows (j%4)*16 + lane/4, 16-byte chunk lane%4
-      row = (j & 3) * 16 + (lane >> 2);
-      col = (j >> 2) * 32 + (lane & 3) * 8;
-    } else {  // d-chunk j/2, rows (j%2)*32 + lane/2, stored half lane%2
-      row = (j & 1) * 32 + (lane >> 1);
-      col = (j >> 1) * 16 + (((lane & 1) ^ ((row >> 3) & 1)) << 3);
+  const __amdgpu_buffer_rsrc_t r =
+      buf_rsrc(src + kvbase + int64_t(key0) * p.kv_stride, uint32_t(p.Skv - key0) * uint32_t(p.kv_stride) * 2u);
+  auto op = [&](auto jjc) __attribute__((always_inline)) {
+    constexpr int jj = decltype(jjc)::value;
+    MXA_LDS void* d = (MXA_LDS void*)(dst + (jj * NW + wave) * 1024);
+    if constexpr (IS_V) {  // d-block j/4 = jj*(NW/4) + wave/4: 64 bytes each
+      buf2lds16(r, ta.lv, uint32_t((jj * (NW / 4) + (NW == 8 ? (wave >> 2) : 0)) * 64), d);
+    } else {  // d-chunk j/2 = jj*(NW/2) + wave/2: 32 bytes each
+      buf2lds16(r, ta.lk, uint32_t((jj * (NW / 2) + (wave >> 1)) * 32), d);
     }
-    int key = key0 + row;
-    key = key < p.Skv ? key : p.Skv - 1;
-    g2lds16(src + int64_t(key) * p.kv_stride + kvbase + col, (MXA_LDS void*)(dst + j * 1024));
-  }
-}
-
-// Liveness byte of one key per lane, always issued (from K itself when there is
-// no mask) so every tile issues the same number of vector-memory ops per wave.
-__device__ __forceinline__ void load_live(const mx_attn_params& p, const uint16_t* k, int key, int& in_range,
-                                          int& byte) {
-  in_range = key < p.Skv;
-  const int kc = key < p.Skv ? key : p.Skv - 1;
-  byte = p.kv_valid ? int(p.kv_valid[kc]) : int(reinterpret_cast<const uint8_t*>(k)[0] | 1);
+  };
+  static_for<NLD>(op);
 }
 
 // S^T = K Q^T for one tile (16 MFMA); the first MFMA of each key block takes a
@@ -232,24 +259,25 @@ __device__ __forceinline__ void rescale(QBlock& X) {
 }
 
 // Scheduling recipes for one 16-MFMA phase: LDS operand reads kept a few MFMAs
-// ahead of use, VALU instructions spread between consecutive MFMAs.
-template <int VALU>
+// ahead of use, and LD vector-memory (LDS-DMA) ops placed one after every
+// fourth MFMA, so no wave issues a burst of DMA ops at once.
+template <int LD>
 __device__ __forceinline__ void sched_k() {
   __builtin_amdgcn_sched_group_barrier(0x100, MXA_KPF, 0);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if constexpr (VALU > 0) __builtin_amdgcn_sched_group_barrier(0x002, VALU, 0);
+    if (i % 4 == 1 && i / 4 < LD) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     if (i < 16 - MXA_KPF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
   }
 }
-template <int VALU>
+template <int LD>
 __device__ __forceinline__ void sched_v() {
   __builtin_amdgcn_sched_group_barrier(0x100, 2 * MXA_VPF, 0);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if constexpr (VALU > 0) __builtin_amdgcn_sched_group_barrier(0x002, VALU, 0);
+    if (i % 4 == 1 && i / 4 < LD) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     if (i < 16 - MXA_VPF) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
   }
 }
@@ -270,33 +298,23 @@ __device__ __forceinline__ void store_block(const QBlock& X, uint16_t* o, const 
     }
 }
 
-// ---------------- W8: 8 waves x 32 queries, two waves per SIMD ----------------
-// NS-stage K/V ring: tile t lives in stage t % NS; at the top of tile t the
-// loads of tile t + NS - 1 go into the stage tile t - 1 used. Each tile issues
-// exactly OPS vector-memory ops per wave, so "tile t has landed" is a counted
-// vmcnt((NS - 2) * OPS) that leaves the younger tiles in flight.
-#ifndef MXA_NS
-#define MXA_NS 2
-#endif
-template <int NS>
+// ---------------- W8: 8 waves x 32 queries, lockstep ----------------
+// Per tile S -> softmax -> P*V on every wave; the two waves of a SIMD overlap
+// only where their phases happen to drift apart. Two-stage K/V ring: tile t
+// lives in stage t % 2 and the loads of tile t + 1 (clamped to the last tile,
+// so the ops are unconditional and interleave with the MFMAs) go into the
+// stage tile t - 1 used.
 __global__ void __launch_bounds__(512, 1)
 flash_bf16_d128_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                    uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign) {
-  constexpr int NW = 8, QT = NW * 32, NLD = 16 / NW, OPS = 2 * NLD;
-  static_assert(NS >= 2 && NS <= 4, "2..4 stages");
+  constexpr int NW = 8, QT = NW * 32, OPS = 2 * (16 / NW);
   __shared__ __align__(16) unsigned char st0[2 * TILEB];
   __shared__ __align__(16) unsigned char st1[2 * TILEB];
-  __shared__ __align__(16) unsigned char st2[2 * TILEB];
-  __shared__ __align__(16) unsigned char st3[2 * TILEB];
-  auto stage = [&](auto i) __attribute__((always_inline)) -> unsigned char* {
-    constexpr int I = decltype(i)::value % NS;
-    if constexpr (I == 0) return st0;
-    else if constexpr (I == 1) return st1;
-    else if constexpr (I == 2) return st2;
-    else return st3;
-  };
+  __shared__ uint64_t live_tiles[kMaxLiveTiles];
+  MXA_CLOCK_BEGIN
   const Lane ln(c);
   const int wave = threadIdx.x >> 6;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int ntq = (p.Sq + QT - 1) / QT;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int head = L / ntq, qtile = L % ntq;
@@ -304,137 +322,153 @@ flash_bf16_d128_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   const int q0 = qtile * QT + wave * 32;
   const int nt = (p.Skv + KT - 1) / KT;
   const int64_t kvbase = int64_t(kvh) * D;
+  const TileAddr ta = tile_addr<NW>(p, wave_u, ln.lane);
 
   QBlock A;
   qblock_init(A, q, p, q0, head, ln, qsign);
-
-  __shared__ uint64_t live_tiles[kMaxLiveTiles];
   auto issue = [&](int t, unsigned char* dst) __attribute__((always_inline)) {
-    load_tile<NW, false>(k, t, dst, p, kvbase, wave, ln.lane);
-    load_tile<NW, true>(v, t, dst + TILEB, p, kvbase, wave, ln.lane);
+    load_tile<NW, false>(k, t, dst, p, kvbase, wave_u, ta);
+    load_tile<NW, true>(v, t, dst + TILEB, p, kvbase, wave_u, ta);
   };
-  issue(0, stage(std::integral_constant<int, 0>{}));
-  if constexpr (NS > 2) if (1 < nt) issue(1, stage(std::integral_constant<int, 1>{}));
-  if constexpr (NS > 3) if (2 < nt) issue(2, stage(std::integral_constant<int, 2>{}));
+  issue(0, st0);
   build_live<NW, KT>(live_tiles, p, nt, wave, ln.lane);
   __syncthreads();  // bitmaps visible (once, before the pipelined loop)
 
-  auto step = [&](int t, auto i) __attribute__((always_inline)) {
-    constexpr int I = decltype(i)::value;
-    const unsigned char* kd = stage(i);
-    const unsigned char* vd = kd + TILEB;
-    // tile t has landed unless it is among the last NS-2 tiles (then wait for all)
-    if (t + NS - 2 < nt) wait_vm_n<(NS - 2) * OPS>();
-    else wait_vm_n<0>();
-    block_sync();
+  auto step = [&](int t, unsigned char* cur, unsigned char* nxt) __attribute__((always_inline)) {
+    wait_vm_n<0>();  // tile t landed
+    block_sync();    // ... for every wave, and tile t - 1's stage is free
     const uint64_t live = tile_live<KT>(live_tiles, p, t);
-    if (t + NS - 1 < nt) issue(t + NS - 1, stage(std::integral_constant<int, I + NS - 1>{}));
-    scores(kd, A, ln);
-    sched_k<0>();
+    issue(t + 1 < nt ? t + 1 : nt - 1, nxt);
+    scores(cur, A, ln);
+    sched_k<OPS>();
     if (live != ~0ull) mask_scores(A, live, ln);
     softmax(A, ln);
     rescale(A);
-    pv(vd, A, ln);
+    pv(cur + TILEB, A, ln);
     sched_v<0>();
   };
-  for (int t = 0; t < nt; t += NS) {
-    step(t, std::integral_constant<int, 0>{});
-    if (t + 1 < nt) step(t + 1, std::integral_constant<int, 1>{});
-    if constexpr (NS > 2) if (t + 2 < nt) step(t + 2, std::integral_constant<int, 2>{});
-    if constexpr (NS > 3) if (t + 3 < nt) step(t + 3, std::integral_constant<int, 3>{});
+  for (int t = 0; t < nt; t += 2) {
+    step(t, st0, st1);
+    if (t + 1 < nt) step(t + 1, st1, st0);
   }
+  wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
   store_block(A, o, p, q0, head, ln);
+  MXA_CLOCK_END
 }
 
-// ---------------- W4S: 4 waves x (2 x 32) queries, staggered blocks ----------------
-__global__ void __launch_bounds__(256, 1)
-flash_bf16_d128_w4s(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                    uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign) {
-  constexpr int NW = 4, QT = NW * 64, NLD = 16 / NW;
-  constexpr int NK = NLD + 1;  // K group: K tile + one liveness byte
+// ---------------- PP: 8 waves x 32 queries, ping-pong groups ----------------
+// Waves w and w + 4 share a SIMD. Group A (waves 0-3) and group B (waves 4-7)
+// run the same per-tile program offset by one period, so in every period one
+// wave of each SIMD issues only MFMA (P(t) V(t), then S(t+1)) and the other only
+// VALU (the online softmax); the SIMD keeps the matrix core busy with the first
+// and fills the issue gaps with the second. Two work-group barriers per tile
+// separate the periods:
+//   period 2t+1: A: P V(t), S(t+1)    B: softmax(t)
+//   period 2t+2: A: softmax(t+1)       B: P V(t), S(t+1)
+// K(t+2) and V(t+1) go into the buffers of K(t) and V(t-1), both last read in
+// period 2t; group A issues all of their DMA ops during its MFMA period 2t+1
+// (8 per wave, one per four MFMAs), and waits for them at the top of tile t+1.
+__global__ void __launch_bounds__(512, 1)
+flash_bf16_d128_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                   uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign) {
+  constexpr int NW = 8, QT = NW * 32;
   __shared__ __align__(16) unsigned char kb0[TILEB];
   __shared__ __align__(16) unsigned char kb1[TILEB];
   __shared__ __align__(16) unsigned char vb0[TILEB];
   __shared__ __align__(16) unsigned char vb1[TILEB];
+  __shared__ uint64_t live_tiles[kMaxLiveTiles];
+  MXA_CLOCK_BEGIN
   const Lane ln(c);
   const int wave = threadIdx.x >> 6;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const bool group_a = wave < 4;
   const int ntq = (p.Sq + QT - 1) / QT;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int head = L / ntq, qtile = L % ntq;
   const int kvh = head / (p.Hq / p.Hkv);
-  const int q0 = qtile * QT + wave * 64;
+  const int q0 = qtile * QT + wave * 32;
   const int nt = (p.Skv + KT - 1) / KT;
   const int64_t kvbase = int64_t(kvh) * D;
+  const TileAddr ta8 = tile_addr<8>(p, wave_u, ln.lane);      // prologue: all 8 waves load
+  const TileAddr ta4 = tile_addr<4>(p, wave_u & 3, ln.lane);  // loop: group A loads
 
-  QBlock A, B;
+  load_tile<NW, false>(k, 0, kb0, p, kvbase, wave_u, ta8);
+  load_tile<NW, true>(v, 0, vb0, p, kvbase, wave_u, ta8);
+  if (nt > 1) load_tile<NW, false>(k, 1, kb1, p, kvbase, wave_u, ta8);
+  QBlock A;
   qblock_init(A, q, p, q0, head, ln, qsign);
-  qblock_init(B, q, p, q0 + 32, head, ln, qsign);
+  build_live<NW, KT>(live_tiles, p, nt, wave, ln.lane);
 
-  // prologue: K(0) (+ liveness) then V(0) in flight
-  load_tile<NW, false>(k, 0, kb0, p, kvbase, wave, ln.lane);
-  int live_in, live_byte;
-  load_live(p, k, ln.lane, live_in, live_byte);
-  load_tile<NW, true>(v, 0, vb0, p, kvbase, wave, ln.lane);
-
-  // Tile t: kcur = K(t), vcur = V(t), vprev = V(t-1); knext/vnext receive K(t+1)/V(t+1).
-  auto step = [&](int t, const unsigned char* kcur, const unsigned char* vcur, const unsigned char* vprev,
-                  unsigned char* knext, unsigned char* vnext, auto first) __attribute__((always_inline)) {
-    constexpr bool FIRST = decltype(first)::value;
-    // top: K(t) and its liveness bytes have landed (V(t) may still be in flight)
-    wait_vm_n<NLD>();
-    __syncthreads();
-    const uint64_t live = __ballot(live_in && live_byte);
-    if (t + 1 < nt) {
-      load_tile<NW, false>(k, t + 1, knext, p, kvbase, wave, ln.lane);
-      load_live(p, k, (t + 1) * KT + ln.lane, live_in, live_byte);
-    }
-    // P1: S_A(t) || softmax_B(t-1)
-    scores(kcur, A, ln);
-    if constexpr (!FIRST) {
-      softmax(B, ln);
-      sched_k<MXA_SVALU>();
-      rescale(B);
+  // MFMA period of tile t: P V(t) then S(t+1). S(t+1) on a stale buffer when
+  // t + 1 == nt is harmless (never read). With LOAD, also the DMA of V(t+1) and
+  // K(t+2) (clamped to the last tile so the ops are unconditional).
+  auto mfma_part = [&](int t, const unsigned char* kc1, const unsigned char* vcur, unsigned char* kfree,
+                       unsigned char* vfree, auto load) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_setprio(1);
+    if constexpr (decltype(load)::value) {
+      load_tile<4, true>(v, t + 1 < nt ? t + 1 : nt - 1, vfree, p, kvbase, wave_u & 3, ta4);
+      pv(vcur, A, ln);
+      sched_v<4>();
+      load_tile<4, false>(k, t + 2 < nt ? t + 2 : nt - 1, kfree, p, kvbase, wave_u & 3, ta4);
+      scores(kc1, A, ln);
+      sched_k<4>();
     } else {
+      pv(vcur, A, ln);
+      sched_v<0>();
+      scores(kc1, A, ln);
       sched_k<0>();
     }
+    __builtin_amdgcn_s_setprio(0);
+  };
+  auto valu_part = [&](int t) __attribute__((always_inline)) {
+    const uint64_t live = tile_live<KT>(live_tiles, p, t);
     if (live != ~0ull) mask_scores(A, live, ln);
-    // P2: P_B V(t-1) || softmax_A(t)
-    if constexpr (!FIRST) pv(vprev, B, ln);
     softmax(A, ln);
-    if constexpr (!FIRST) sched_v<MXA_SVALU>();
-    // mid: everyone is done with V(t-1); V(t) has landed
-    wait_vm_n<NK>();
-    __syncthreads();
-    if (t + 1 < nt) load_tile<NW, true>(v, t + 1, vnext, p, kvbase, wave, ln.lane);
-    // P3: S_B(t), then the rescale of O_A
-    scores(kcur, B, ln);
-    sched_k<0>();
     rescale(A);
-    if (live != ~0ull) mask_scores(B, live, ln);
-    // P4: P_A V(t)
-    pv(vcur, A, ln);
-    sched_v<0>();
   };
 
-  step(0, kb0, vb0, vb1, kb1, vb1, std::true_type{});
-  for (int t = 1; t < nt; t += 2) {
-    step(t, kb1, vb1, vb0, kb0, vb0, std::false_type{});
-    if (t + 1 < nt) step(t + 1, kb0, vb0, vb1, kb1, vb1, std::false_type{});
+  wait_vm_n<0>();
+  __syncthreads();  // K(0), V(0), K(1) and the liveness bitmaps are visible
+  if (group_a) {    // period -1: S_A(0)
+    scores(kb0, A, ln);
+    sched_k<0>();
   }
-  // drain: softmax_B(nt-1), P_B V(nt-1)
-  softmax(B, ln);
-  rescale(B);
-  pv((nt - 1) & 1 ? vb1 : vb0, B, ln);
+  block_sync();
+  if (group_a) {    // period 0: A softmax(0), B S_B(0)
+    valu_part(0);
+  } else {
+    scores(kb0, A, ln);
+    sched_k<0>();
+  }
 
+  // Tile t: kc1 = K(t+1), vcur = V(t); kfree / vfree receive K(t+2) / V(t+1).
+  auto tile = [&](int t, const unsigned char* kc1, const unsigned char* vcur, unsigned char* kfree,
+                  unsigned char* vfree) __attribute__((always_inline)) {
+    wait_vm_n<0>();  // group A: K(t+1), V(t) landed
+    block_sync();
+    if (group_a) mfma_part(t, kc1, vcur, kfree, vfree, std::true_type{});
+    else valu_part(t);
+    block_sync();
+    if (group_a) {
+      if (t + 1 < nt) valu_part(t + 1);
+    } else {
+      mfma_part(t, kc1, vcur, kfree, vfree, std::false_type{});
+    }
+  };
+  for (int t = 0; t < nt; t += 2) {
+    tile(t, kb1, vb0, kb0, vb1);
+    if (t + 1 < nt) tile(t + 1, kb0, vb1, kb1, vb0);
+  }
+  wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
   store_block(A, o, p, q0, head, ln);
-  store_block(B, o, p, q0 + 32, head, ln);
+  MXA_CLOCK_END
 }
 
 }  // namespace
 
 // Launch the fast path. Preconditions (checked by the caller): D == 128,
 // non-causal, q/k/v 16-byte aligned with token strides % 8 == 0, o 4-byte
-// aligned with o_stride % 2 == 0.
+// aligned with o_stride % 2 == 0, Skv * kv_stride * 2 < 2^32.
 hipError_t launch_flash_bf16_d128(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                                   const mx_attn_params& p, hipStream_t s) {
   const float c = __builtin_fabsf(p.scale) * kLog2e;
@@ -443,10 +477,10 @@ hipError_t launch_flash_bf16_d128(const uint16_t* q, const uint16_t* k, const ui
   const int ntq = (p.Sq + QT - 1) / QT;
   const int64_t blocks = int64_t(ntq) * p.Hq;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-#if MXA_BF16_KIND == 8
-  hipLaunchKernelGGL(flash_bf16_d128_w8<MXA_NS>, dim3(unsigned(blocks)), dim3(512), 0, s, q, k, v, o, p, c, qsign);
+#if MXA_BF16_KIND == 9
+  hipLaunchKernelGGL(flash_bf16_d128_pp, dim3(unsigned(blocks)), dim3(512), 0, s, q, k, v, o, p, c, qsign);
 #else
-  hipLaunchKernelGGL(flash_bf16_d128_w4s, dim3(unsigned(blocks)), dim3(256), 0, s, q, k, v, o, p, c, qsign);
+  hipLaunchKernelGGL(flash_bf16_d128_w8, dim3(unsigned(blocks)), dim3(512), 0, s, q, k, v, o, p, c, qsign);
 #endif
   return hipGetLastError();
 }
