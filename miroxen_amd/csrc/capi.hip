@@ -118,7 +118,7 @@ extern "C" {
 
 const char* mx_last_error(void) { return g_err; }
 
-const char* mx_version(void) { return "miroxen_amd gfx950 bf16:pp8x32q-k64 sage:w8x32q-k64"; }
+const char* mx_version(void) { return "miroxen_amd gfx950 bf16:pp8x32q-k64 sage:w8x32q-k64-int8fp8"; }
 
 int mx_flash_attn(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p, void* stream) {
   mx_attn_params a;

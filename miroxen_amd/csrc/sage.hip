@@ -241,6 +241,14 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
 // per-lane registers plus compile-time offsets, bank-conflict free):
 //   K int8: [4 d-chunks of 32][64 rows][2 halves of 16 B], half XOR row bit 5;
 //   V^T e4m3: [128 channel rows][64 B], 16-byte chunk XOR ((row >> 2) & 3).
+// Tiles arrive by buffer_load ... lds (no VGPR staging), one K and one V^T op per
+// wave per tile, placed between the score MFMAs of the previous tile.
+//
+// Two work-group schedules (MXA_SAGE_KIND): 8 (default) lockstep, every wave
+// runs S -> softmax -> P*V per tile; 9 ping-pong, as the BF16 kernel's default.
+// The softmax here is the larger share of the work (the INT8/FP8 MFMAs take half
+// the cycles of BF16 ones), and a single wave alone on a SIMD runs it slower than
+// two interleaved waves, so lockstep measures ~10% faster.
 
 constexpr int KT = 64;
 constexpr int KTILEB = KT * D;        // 8 KB int8 K tile
@@ -254,31 +262,52 @@ constexpr i32x16 kScoreBias16 = {kScoreBias, kScoreBias, kScoreBias, kScoreBias,
 #ifndef MXA_SAGE_NS
 #define MXA_SAGE_NS 2
 #endif
+#ifndef MXA_SAGE_KIND
+#define MXA_SAGE_KIND 8
+#endif
 
 // Score row m of key block kb -> key within the 64-key tile.
 __device__ __forceinline__ int kperm(int kb, int m) {
   return ((m >> 2) & 1) * 32 + kb * 16 + (m >> 3) * 4 + (m & 3);
 }
 
+// DMA of one tile (K 8 KB + V^T 8 KB, 8 ops of 1 KB each) by NW waves; op j:
+// K rows (j&1)*32 + lane/2 of d-chunk j/2 (16-byte half XOR row bit 5), V^T
+// channel rows j*16 + lane/4 (16-byte chunk XOR ((row >> 2) & 3)); wave w issues
+// ops j = jj*NW + w. Per-head buffer resources; the per-lane part of each address
+// is loop-invariant (NW even, so j&1 == w&1), the tile and op parts are scalar.
+struct SageAddr {
+  __amdgpu_buffer_rsrc_t rk, rv;
+  uint32_t lk, lv;  // per-lane byte offsets
+};
+__device__ __forceinline__ SageAddr sage_addr(const int8_t* ki, const uint8_t* vt, int kvh, int64_t skv_pad, int wave,
+                                              int lane) {
+  SageAddr a;
+  a.rk = buf_rsrc(ki + int64_t(kvh) * skv_pad * D, uint32_t(skv_pad * D));
+  a.rv = buf_rsrc(vt + int64_t(kvh) * D * skv_pad, uint32_t(skv_pad * D));
+  const int krow = (wave & 1) * 32 + (lane >> 1);
+  a.lk = uint32_t(krow * D + (((lane & 1) ^ ((krow >> 5) & 1)) << 4));
+  const int vrow = lane >> 2;  // + j*16: scalar part (does not change the XOR term)
+  a.lv = uint32_t(vrow) * uint32_t(skv_pad) + uint32_t(((lane & 3) ^ ((vrow >> 2) & 3)) << 4);
+  return a;
+}
+// K tile tk into kdst and V^T tile tv into vdst.
 template <int NW>
-__device__ __forceinline__ void sage_load_tile(const int8_t* ki, const uint8_t* vt, int t, unsigned char* dst,
-                                               int kvh, int64_t skv_pad, int wave, int lane) {
-  const int8_t* kg = ki + (int64_t(kvh) * skv_pad + int64_t(t) * KT) * D;
-  const uint8_t* vg = vt + int64_t(kvh) * D * skv_pad + int64_t(t) * KT;
-#pragma unroll
-  for (int jj = 0; jj < 8 / NW; ++jj) {  // K: op j = d-chunk j/2, rows (j%2)*32 + lane/2
-    const int j = jj * NW + wave;
-    const int row = (j & 1) * 32 + (lane >> 1);
-    const int h = (lane & 1) ^ ((row >> 5) & 1);
-    g2lds16(kg + row * D + (j >> 1) * 32 + h * 16, (MXA_LDS void*)(dst + j * 1024));
-  }
-#pragma unroll
-  for (int jj = 0; jj < 8 / NW; ++jj) {  // V^T: op j = channel rows j*16 + lane/4
-    const int j = jj * NW + wave;
-    const int row = j * 16 + (lane >> 2);
-    const int lc = (lane & 3) ^ ((row >> 2) & 3);
-    g2lds16(vg + int64_t(row) * skv_pad + lc * 16, (MXA_LDS void*)(dst + KTILEB + j * 1024));
-  }
+__device__ __forceinline__ void sage_load_tile(const SageAddr& a, int tk, int tv, unsigned char* kdst,
+                                               unsigned char* vdst, int wave, int64_t skv_pad) {
+  static_for<8 / NW>([&](auto jjc) __attribute__((always_inline)) {
+    const int j = decltype(jjc)::value * NW + wave;
+    buf2lds16(a.rk, a.lk, uint32_t((j >> 1) * 32 + tk * (KT * D)), (MXA_LDS void*)(kdst + j * 1024));
+    buf2lds16(a.rv, a.lv, uint32_t(j * 16) * uint32_t(skv_pad) + uint32_t(tv * KT), (MXA_LDS void*)(vdst + j * 1024));
+  });
+}
+// K tile tk only.
+template <int NW>
+__device__ __forceinline__ void sage_load_k(const SageAddr& a, int tk, unsigned char* kdst, int wave) {
+  static_for<8 / NW>([&](auto jjc) __attribute__((always_inline)) {
+    const int j = decltype(jjc)::value * NW + wave;
+    buf2lds16(a.rk, a.lk, uint32_t((j >> 1) * 32 + tk * (KT * D)), (MXA_LDS void*)(kdst + j * 1024));
+  });
 }
 
 template <int NS>
@@ -308,8 +337,10 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   const int q0 = qtile * QT + wave * 32;
   const int nt = (p.Skv + KT - 1) / KT;
 
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const SageAddr sa = sage_addr(ki, vt, kvh, skv_pad, wave_u, lane);
   auto issue = [&](int t, unsigned char* dst) __attribute__((always_inline)) {
-    sage_load_tile<NW>(ki, vt, t, dst, kvh, skv_pad, wave, lane);
+    sage_load_tile<NW>(sa, t, t, dst, dst + KTILEB, wave_u, skv_pad);
   };
   issue(0, stage(std::integral_constant<int, 0>{}));
   if constexpr (NS > 2) if (1 < nt) issue(1, stage(std::integral_constant<int, 1>{}));
@@ -339,7 +370,10 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
 #pragma unroll
   for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
   float m = -__builtin_inff(), l = 0.f;
-  constexpr int kDead = -2147483647 - 1;
+  // Dead keys get the bits of -inf: below every biased score as an integer (so the
+  // integer max skips them) and, as a float, exp2(fma(-inf, sc, nm)) = 0 exactly
+  // for sc > 0 (sc is clamped to >= 1e-30, which moves no live exponent).
+  constexpr int kDead = int(0xFF800000u);
 
   auto step = [&](int t, auto i) __attribute__((always_inline)) {
     const unsigned char* sd = stage(i);
@@ -347,7 +381,8 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
     else wait_vm_n<0>();
     block_sync();
     const uint64_t live = tile_live<KT>(live_tiles, p, t);
-    if (t + NS - 1 < nt) issue(t + NS - 1, stage(std::integral_constant<int, decltype(i)::value + NS - 1>{}));
+    // tile index clamped: the two DMA ops are unconditional and interleave with the MFMAs
+    issue(t + NS - 1 < nt ? t + NS - 1 : nt - 1, stage(std::integral_constant<int, decltype(i)::value + NS - 1>{}));
     const float ksc = kscale[t];
 
     // ---- S^T = K Q^T (int32, exact) ----
@@ -365,6 +400,7 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (j == 1 || j == 4) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       if (j < 5) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
 
@@ -381,7 +417,7 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
 #pragma unroll
       for (int ii = 0; ii < 16; ++ii) im = max(im, s[kb][ii]);
     im = max(im, other_half_i(im));
-    const float sc = qscale * ksc;
+    const float sc = fmaxf(qscale * ksc, 1e-30f);
     const float tmax = im == kDead ? -__builtin_inff() : float(im - kScoreBias) * sc;
     const float mnew = tmax > m + kSageHeadroom ? tmax : m;
     const float alpha = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
@@ -410,8 +446,7 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
         pf[w] = __builtin_amdgcn_cvt_pk_fp8_f32(e2, e3, int(lo), true);
       }
     };
-    if (live == ~0ull) pack(std::false_type{});
-    else pack(std::true_type{});  // dead keys contribute exactly 0 (even when sc == 0)
+    pack(std::false_type{});
     ts += other_half(ts);
     l = l * alpha + ts;
     if (!__all(alpha == 1.f)) {
@@ -441,6 +476,202 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
     if constexpr (NS > 3) if (t + 3 < nt) step(t + 3, std::integral_constant<int, 3>{});
   }
 
+  wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
+  // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----
+  if (row < p.Sq) {
+    const float* vah = va + kvh * D;
+    const float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
+    uint16_t* dst = o + int64_t(row) * p.o_stride + head * D + h * 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + g * 8 + h * 4;
+        const f32x4 sv = *reinterpret_cast<const f32x4*>(vah + d);
+        uint32_t* d32 = reinterpret_cast<uint32_t*>(dst + db * 32 + g * 8);
+        d32[0] = pack_bf16x2(acc[db][g * 4] * sv[0] * inv, acc[db][g * 4 + 1] * sv[1] * inv);
+        d32[1] = pack_bf16x2(acc[db][g * 4 + 2] * sv[2] * inv, acc[db][g * 4 + 3] * sv[3] * inv);
+      }
+  }
+}
+
+// ---------------- ping-pong variant ----------------
+// Same data flow, but waves w and w + 4 (one SIMD) run the per-tile program one
+// period apart: in each period one issues the MFMAs (P V(t), S(t+1)) while the
+// other runs the softmax, separated by two work-group barriers per tile:
+//   period 2t+1: A: P V(t), S(t+1)    B: softmax(t)
+//   period 2t+2: A: softmax(t+1)       B: P V(t), S(t+1)
+// Group A issues the DMA of K(t+2) and V(t+1) (into the buffers of K(t) and
+// V(t-1), last read in period 2t) between its MFMAs in period 2t+1.
+__global__ void __launch_bounds__(512, 1)
+sage_attn_d128_pp(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, const uint8_t* __restrict__ vt,
+                  const float* __restrict__ qs, const float* __restrict__ ks, const float* __restrict__ va,
+                  uint16_t* __restrict__ o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad) {
+  constexpr int NW = 8, QT = NW * 32;
+  __shared__ __align__(16) unsigned char kb0[KTILEB];
+  __shared__ __align__(16) unsigned char kb1[KTILEB];
+  __shared__ __align__(16) unsigned char vb0[VTILEB];
+  __shared__ __align__(16) unsigned char vb1[VTILEB];
+  __shared__ uint64_t live_tiles[kMaxLiveTiles];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 31, h = lane >> 5;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const bool group_a = wave < 4;
+  const int ntq = (p.Sq + QT - 1) / QT;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int head = L / ntq, qtile = L % ntq;
+  const int kvh = head / (p.Hq / p.Hkv);
+  const int q0 = qtile * QT + wave * 32;
+  const int nt = (p.Skv + KT - 1) / KT;
+  const SageAddr sa8 = sage_addr(ki, vt, kvh, skv_pad, wave_u, lane);
+  const SageAddr sa4 = sage_addr(ki, vt, kvh, skv_pad, wave_u & 3, lane);
+  sage_load_tile<8>(sa8, 0, 0, kb0, vb0, wave_u, skv_pad);
+  if (nt > 1) sage_load_k<8>(sa8, 1, kb1, wave_u);
+
+  const int row = q0 + n;  // < sq_pad (sq_pad is a multiple of QT)
+  i32x4 qf[4];
+  {
+    const int8_t* src = qi + (int64_t(head) * sq_pad + row) * D + h * 16;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) qf[cc] = *reinterpret_cast<const i32x4*>(src + cc * 32);
+  }
+  const float qscale = qs[int64_t(head) * (sq_pad / 16) + row / 16];
+  const float* kscale = ks + int64_t(kvh) * (skv_pad / KT);
+  build_live<NW, KT>(live_tiles, p, nt, wave, lane);
+
+  const int krow = kperm(0, n);
+  const int kbase = krow * 32 + ((h ^ ((krow >> 5) & 1)) << 4);
+  const int vsw = (n >> 2) & 3;
+  const int vbase0 = n * 64 + (((2 * h) ^ vsw) << 4);
+  const int vbase1 = n * 64 + (((2 * h + 1) ^ vsw) << 4);
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
+  float m = -__builtin_inff(), l = 0.f;
+  // Dead keys get the bits of -inf: below every biased score as an integer (so the
+  // integer max skips them) and, as a float, exp2(fma(-inf, sc, nm)) = 0 exactly
+  // for sc > 0 (sc is clamped to >= 1e-30, which moves no live exponent).
+  constexpr int kDead = int(0xFF800000u);
+  i32x16 s[2];  // biased int32 scores of the pending tile
+  i32x8 pf;     // P of the pending tile (e4m3)
+
+  auto scores = [&](const unsigned char* kd, auto ld) __attribute__((always_inline)) {
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const i32x4 a = *reinterpret_cast<const i32x4*>(kd + kbase + cc * 2048 + kb * 512);
+        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[cc], cc == 0 ? kScoreBias16 : s[kb], 0, 0, 0);
+      }
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (decltype(ld)::value && (j == 1 || j == 5)) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (j < 5) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  };
+  auto pv = [&](const unsigned char* vd, auto ld) __attribute__((always_inline)) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const i32x4 a0 = *reinterpret_cast<const i32x4*>(vd + vbase0 + db * 2048);
+      const i32x4 a1 = *reinterpret_cast<const i32x4*>(vd + vbase1 + db * 2048);
+      const i32x8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, pf, acc[db], 0, 0, 0, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (decltype(ld)::value) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (j < 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+  };
+  auto softmax = [&](int t) __attribute__((always_inline)) {
+    const uint64_t live = tile_live<KT>(live_tiles, p, t);
+    if (live != ~0ull) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int ii = 0; ii < 16; ++ii)
+          if (!((live >> (h * 32 + kb * 16 + ii)) & 1)) s[kb][ii] = kDead;
+    }
+    int im = s[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int ii = 0; ii < 16; ++ii) im = max(im, s[kb][ii]);
+    im = max(im, other_half_i(im));
+    const float sc = fmaxf(qscale * kscale[t], 1e-30f);
+    const float tmax = im == kDead ? -__builtin_inff() : float(im - kScoreBias) * sc;
+    const float mnew = tmax > m + kSageHeadroom ? tmax : m;
+    const float alpha = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+    m = mnew;
+    const float nm =
+        mnew == -__builtin_inff() ? -__builtin_inff() : (kLog2_448 - kSageHeadroom - mnew) - 12582912.f * sc;
+    float ts = 0.f;
+    auto pexp = [&](int si, auto masked) __attribute__((always_inline)) -> float {
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(__int_as_float(si), sc, nm));
+      if constexpr (decltype(masked)::value) return si == kDead ? 0.f : e;
+      return e;
+    };
+    auto pack = [&](auto masked) __attribute__((always_inline)) {
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        const int kb = w >> 2, i0 = (w & 3) * 4;
+        const float e0 = pexp(s[kb][i0], masked), e1 = pexp(s[kb][i0 + 1], masked);
+        const float e2 = pexp(s[kb][i0 + 2], masked), e3 = pexp(s[kb][i0 + 3], masked);
+        ts += (e0 + e1) + (e2 + e3);
+        const uint32_t lo = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(e0, e1, 0, false));
+        pf[w] = __builtin_amdgcn_cvt_pk_fp8_f32(e2, e3, int(lo), true);
+      }
+    };
+    pack(std::false_type{});
+    ts += other_half(ts);
+    l = l * alpha + ts;
+    if (!__all(alpha == 1.f)) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+    }
+  };
+  // MFMA period of tile t (S(t+1) on a stale buffer when t + 1 == nt is never read).
+  auto mfma_part = [&](int t, const unsigned char* kc1, const unsigned char* vcur, unsigned char* kfree,
+                       unsigned char* vfree, auto ld) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_setprio(1);
+    if constexpr (decltype(ld)::value)  // K(t+2), V(t+1), clamped so the ops are unconditional
+      sage_load_tile<4>(sa4, t + 2 < nt ? t + 2 : nt - 1, t + 1 < nt ? t + 1 : nt - 1, kfree, vfree, wave_u & 3,
+                        skv_pad);
+    pv(vcur, ld);
+    scores(kc1, ld);
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  wait_vm_n<0>();
+  __syncthreads();  // K(0), V(0), K(1) and the liveness bitmaps are visible
+  if (group_a) scores(kb0, std::false_type{});  // period -1: S_A(0)
+  block_sync();
+  if (group_a) softmax(0);  // period 0: A softmax(0), B S_B(0)
+  else scores(kb0, std::false_type{});
+
+  // Tile t: kc1 = K(t+1), vcur = V(t); kfree / vfree receive K(t+2) / V(t+1).
+  auto tile = [&](int t, const unsigned char* kc1, const unsigned char* vcur, unsigned char* kfree,
+                  unsigned char* vfree) __attribute__((always_inline)) {
+    wait_vm_n<0>();  // group A: its DMA of K(t+1), V(t) landed
+    block_sync();
+    if (group_a) mfma_part(t, kc1, vcur, kfree, vfree, std::true_type{});
+    else softmax(t);
+    block_sync();
+    if (group_a) {
+      if (t + 1 < nt) softmax(t + 1);
+    } else {
+      mfma_part(t, kc1, vcur, kfree, vfree, std::false_type{});
+    }
+  };
+  for (int t = 0; t < nt; t += 2) {
+    tile(t, kb1, vb0, kb0, vb1);
+    if (t + 1 < nt) tile(t + 1, kb0, vb1, kb1, vb0);
+  }
+  wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
   // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----
   if (row < p.Sq) {
     const float* vah = va + kvh * D;
@@ -514,7 +745,11 @@ hipError_t launch_sage_attend(uint16_t* o, const mx_attn_params& p, const char* 
   const int ntq = (p.Sq + QT - 1) / QT;
   const int64_t blocks = int64_t(ntq) * p.Hq;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+#if MXA_SAGE_KIND == 9
+  hipLaunchKernelGGL(sage_attn_d128_pp, dim3(unsigned(blocks)), dim3(512), 0, s,
+#else
   hipLaunchKernelGGL((sage_attn_d128<MXA_SAGE_NS>), dim3(unsigned(blocks)), dim3(512), 0, s,
+#endif
                      reinterpret_cast<const int8_t*>(ws + L.qi), reinterpret_cast<const int8_t*>(ws + L.ki),
                      reinterpret_cast<const uint8_t*>(ws + L.vt), reinterpret_cast<const float*>(ws + L.qs),
                      reinterpret_cast<const float*>(ws + L.ks), reinterpret_cast<const float*>(ws + L.va), o, p,
