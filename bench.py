@@ -84,6 +84,38 @@ def cpu_baseline(q, k, v, mask, S, H, D, budget_s: float = 12.0):
                       f"full call extrapolated {dt * S / n * 1e3:.0f} ms"}
 
 
+def _only(which: str, n: int) -> int:
+    """Run one kernel n times on the bench inputs (for rocprofv3 --pmc passes)."""
+    import torch
+
+    from miroxen_amd import AttnParams, flash_attn, flash_attn_fp8_workspace, sage_attend, sage_quantize
+    from miroxen_amd.synth import CONFIGS, make_inputs
+    dev = torch.device("cuda:0")
+    if which == "copy":
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(n):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        return 0
+    cfg = CONFIGS[2 if which == "bf16" else 3]
+    q, k, v, m = make_inputs(cfg, seed=2 if which == "bf16" else 3, device=dev)
+    p = AttnParams(Sq=cfg.S, Skv=cfg.S, Hq=cfg.H, Hkv=cfg.H, D=cfg.D, kv_valid=m)
+    o = torch.empty_like(q)
+    ws = torch.empty(flash_attn_fp8_workspace(p), dtype=torch.uint8, device=dev)
+    if which == "sage":
+        sage_quantize(q, k, v, p, ws)
+    for _ in range(n):
+        if which == "bf16":
+            flash_attn(q, k, v, o, p)
+        elif which == "sage":
+            sage_attend(o, p, ws)
+        else:
+            sage_quantize(q, k, v, p, ws)
+    torch.cuda.synchronize()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -92,6 +124,9 @@ def main() -> int:
     ap.add_argument("--warm-seconds", type=float, default=0.5,
                     help="minimum seconds of untimed back-to-back calls before each timed region")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=["bf16", "sage", "prologue", "copy"],
+                    help="profiling driver: run just this kernel --steps times (no warm-up, no JSON); "
+                         "'copy' is a 256 MiB device copy for calibrating HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the attention on one GPU only (no multi-GPU path); "
@@ -99,6 +134,9 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.only:
+        return _only(args.only, args.steps)
 
     from miroxen_amd import (AttnParams, flash_attn, flash_attn_fp8, flash_attn_fp8_workspace, sage_attend,
                              sage_quantize, version)
