@@ -202,13 +202,18 @@ __device__ __forceinline__ void pv(const unsigned char* vd, QBlock& X, const Lan
 }
 
 // Dead keys (padding mask, tail) -> score -inf.
+// Score i of key block kb is key kb*32 + (i>>3)*16 + 8h + (i&7): shift the bitmap
+// by 8h once, then every test is a compile-time bit position (no per-lane masks).
 __device__ __forceinline__ void mask_scores(QBlock& X, uint64_t live, const Lane& ln) {
+  const uint64_t lv = live >> (ln.h * 8);
+  const uint32_t lo = uint32_t(lv), hi = uint32_t(lv >> 32);
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int key = kb * 32 + (i >> 3) * 16 + ln.h * 8 + (i & 7);
-      if (!((live >> key) & 1)) X.s[kb][i] = -__builtin_inff();
+      const int bit = kb * 32 + (i >> 3) * 16 + (i & 7);
+      const uint32_t w = bit < 32 ? lo : hi;
+      if (!((w >> (bit & 31)) & 1u)) X.s[kb][i] = -__builtin_inff();
     }
 }
 
@@ -220,6 +225,8 @@ __device__ __forceinline__ void mask_scores(QBlock& X, uint64_t live, const Lane
 constexpr float kLazyMax = 8.f;
 __device__ __forceinline__ void softmax(QBlock& X, const Lane& ln) {
   const float c = ln.c;
+  // four independent max chains (a single wave runs this alone in the ping-pong
+  // schedule, so dependent-issue latency is not hidden by a second wave)
   float mx = X.s[0][0];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)

@@ -15,6 +15,13 @@
 
 namespace mxa {
 
+#ifdef MXA_PPT
+__device__ uint64_t* g_ppt = nullptr;
+extern "C" int mx_debug_ppt(void* buf) {
+  return hipMemcpyToSymbol(HIP_SYMBOL(g_ppt), &buf, sizeof(buf)) == hipSuccess ? 0 : -2;
+}
+#endif
+
 namespace {
 
 constexpr int D = 128;
@@ -405,11 +412,14 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
     }
 
     if (live != ~0ull) {
+      // this lane's 32 keys are bits 32h .. 32h+31: select the word once, then
+      // every test is a compile-time bit position (no per-lane mask registers)
+      const uint32_t lw = h ? uint32_t(live >> 32) : uint32_t(live);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int ii = 0; ii < 16; ++ii)
-          if (!((live >> (h * 32 + kb * 16 + ii)) & 1)) s[kb][ii] = kDead;
+          if (!((lw >> (kb * 16 + ii)) & 1u)) s[kb][ii] = kDead;
     }
     int im = s[0][0];
 #pragma unroll
@@ -590,11 +600,14 @@ sage_attn_d128_pp(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, 
   auto softmax = [&](int t) __attribute__((always_inline)) {
     const uint64_t live = tile_live<KT>(live_tiles, p, t);
     if (live != ~0ull) {
+      // this lane's 32 keys are bits 32h .. 32h+31: select the word once, then
+      // every test is a compile-time bit position (no per-lane mask registers)
+      const uint32_t lw = h ? uint32_t(live >> 32) : uint32_t(live);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int ii = 0; ii < 16; ++ii)
-          if (!((live >> (h * 32 + kb * 16 + ii)) & 1)) s[kb][ii] = kDead;
+          if (!((lw >> (kb * 16 + ii)) & 1u)) s[kb][ii] = kDead;
     }
     int im = s[0][0];
 #pragma unroll
@@ -654,24 +667,41 @@ sage_attn_d128_pp(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, 
   else scores(kb0, std::false_type{});
 
   // Tile t: kc1 = K(t+1), vcur = V(t); kfree / vfree receive K(t+2) / V(t+1).
+#ifdef MXA_PPT
+  uint64_t pt0 = 0, pt1 = 0, pt2 = 0, pt3 = 0, pt4 = 0;
+#define MXA_PT(v) do { if (t == 20) { __builtin_amdgcn_sched_barrier(0); v = __builtin_amdgcn_s_memtime(); __builtin_amdgcn_sched_barrier(0); } } while (0)
+#else
+#define MXA_PT(v) do { } while (0)
+#endif
   auto tile = [&](int t, const unsigned char* kc1, const unsigned char* vcur, unsigned char* kfree,
                   unsigned char* vfree) __attribute__((always_inline)) {
+    MXA_PT(pt0);
     wait_vm_n<0>();  // group A: its DMA of K(t+1), V(t) landed
     block_sync();
+    MXA_PT(pt1);
     if (group_a) mfma_part(t, kc1, vcur, kfree, vfree, std::true_type{});
     else softmax(t);
+    MXA_PT(pt2);
     block_sync();
+    MXA_PT(pt3);
     if (group_a) {
       if (t + 1 < nt) softmax(t + 1);
     } else {
       mfma_part(t, kc1, vcur, kfree, vfree, std::false_type{});
     }
+    MXA_PT(pt4);
   };
   for (int t = 0; t < nt; t += 2) {
     tile(t, kb1, vb0, kb0, vb1);
     if (t + 1 < nt) tile(t + 1, kb0, vb1, kb1, vb0);
   }
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
+#ifdef MXA_PPT
+  if (lane == 0 && g_ppt) {
+    uint64_t* d = g_ppt + (int64_t(blockIdx.x) * 8 + wave) * 5;
+    d[0] = pt0; d[1] = pt1; d[2] = pt2; d[3] = pt3; d[4] = pt4;
+  }
+#endif
   // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----
   if (row < p.Sq) {
     const float* vah = va + kvh * D;
