@@ -106,7 +106,7 @@ int fp8_ok(const void* q, const void* k, const void* v, const void* o, const mx_
 }
 
 bool fast_bf16_ok(const void* q, const void* k, const void* v, const void* o, const mx_attn_params& p) {
-  return p.D == 128 && !p.causal && p.q_stride % 8 == 0 && p.kv_stride % 8 == 0 && p.o_stride % 2 == 0 &&
+  return p.D == 128 && p.q_stride % 8 == 0 && p.kv_stride % 8 == 0 && p.o_stride % 2 == 0 &&
          aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 4) &&
          (!p.kv_valid || p.Skv <= kMaxMaskedSkv) &&
          int64_t(p.Skv) * p.kv_stride * 2 < (int64_t(1) << 32);  // K/V tiles read through 32-bit buffer offsets

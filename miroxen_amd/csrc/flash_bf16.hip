@@ -204,17 +204,39 @@ __device__ __forceinline__ void pv(const unsigned char* vd, QBlock& X, const Lan
 // Dead keys (padding mask, tail) -> score -inf.
 // Score i of key block kb is key kb*32 + (i>>3)*16 + 8h + (i&7): shift the bitmap
 // by 8h once, then every test is a compile-time bit position (no per-lane masks).
-__device__ __forceinline__ void mask_scores(QBlock& X, uint64_t live, const Lane& ln) {
+// `rel` is the last key of the tile this lane's query may see (causal; >= 63 when
+// every key is visible), so key index kk is kept iff kk <= rel.
+__device__ __forceinline__ void mask_scores(QBlock& X, uint64_t live, int rel, const Lane& ln) {
   const uint64_t lv = live >> (ln.h * 8);
   const uint32_t lo = uint32_t(lv), hi = uint32_t(lv >> 32);
+  const int relh = rel - ln.h * 8;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int bit = kb * 32 + (i >> 3) * 16 + (i & 7);
       const uint32_t w = bit < 32 ? lo : hi;
-      if (!((w >> (bit & 31)) & 1u)) X.s[kb][i] = -__builtin_inff();
+      if (!((w >> (bit & 31)) & 1u) || bit > relh) X.s[kb][i] = -__builtin_inff();
     }
+}
+
+// Causal limit of one lane's query (row) for tile t: the last visible key index
+// within the tile, clamped to [-1, 63] (reference: key j visible iff
+// j <= q_offset + row, attention.cu:108).
+__device__ __forceinline__ int causal_rel(const mx_attn_params& p, int row, int t) {
+  const int64_t r = int64_t(p.q_offset) + row - int64_t(t) * KT;
+  return r < -1 ? -1 : (r > KT - 1 ? KT - 1 : int(r));
+}
+
+// Key tiles one work-group of queries [qbeg, qbeg + QT) needs: all of them, or
+// under the causal mask those up to key q_offset + min(qbeg + QT, Sq) - 1.
+__device__ __forceinline__ int tiles_needed(const mx_attn_params& p, int qbeg, int QT) {
+  const int nt = (p.Skv + KT - 1) / KT;
+  if (!p.causal) return nt;
+  const int64_t last = int64_t(p.q_offset) + (qbeg + QT < p.Sq ? qbeg + QT : p.Sq);  // exclusive
+  if (last <= 0) return 0;
+  const int64_t e = last < p.Skv ? last : p.Skv;
+  return int((e + KT - 1) / KT);
 }
 
 // Branch-free online softmax (base 2) of one tile. X.m is the running max in
@@ -324,15 +346,20 @@ flash_bf16_d128_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int ntq = (p.Sq + QT - 1) / QT;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int head = L / ntq, qtile = L % ntq;
+  // causal: query tiles with the most key tiles first
+  const int head = L / ntq, qtile = p.causal ? ntq - 1 - L % ntq : L % ntq;
   const int kvh = head / (p.Hq / p.Hkv);
   const int q0 = qtile * QT + wave * 32;
-  const int nt = (p.Skv + KT - 1) / KT;
+  const int nt = tiles_needed(p, qtile * QT, QT);
   const int64_t kvbase = int64_t(kvh) * D;
   const TileAddr ta = tile_addr<NW>(p, wave_u, ln.lane);
 
   QBlock A;
   qblock_init(A, q, p, q0, head, ln, qsign);
+  if (nt == 0) {  // causal: no visible key for any query of the work-group -> 0
+    store_block(A, o, p, q0, head, ln);
+    return;
+  }
   auto issue = [&](int t, unsigned char* dst) __attribute__((always_inline)) {
     load_tile<NW, false>(k, t, dst, p, kvbase, wave_u, ta);
     load_tile<NW, true>(v, t, dst + TILEB, p, kvbase, wave_u, ta);
@@ -348,7 +375,8 @@ flash_bf16_d128_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
     issue(t + 1 < nt ? t + 1 : nt - 1, nxt);
     scores(cur, A, ln);
     sched_k<OPS>();
-    if (live != ~0ull) mask_scores(A, live, ln);
+    const bool diag = p.causal && int64_t(p.q_offset) + q0 - int64_t(t) * KT < KT - 1;  // wave-uniform
+    if (live != ~0ull || diag) mask_scores(A, live, diag ? causal_rel(p, q0 + ln.n, t) : KT - 1, ln);
     softmax(A, ln);
     rescale(A);
     pv(cur + TILEB, A, ln);
@@ -391,18 +419,24 @@ flash_bf16_d128_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   const bool group_a = wave < 4;
   const int ntq = (p.Sq + QT - 1) / QT;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int head = L / ntq, qtile = L % ntq;
+  // causal: query tiles with the most key tiles first
+  const int head = L / ntq, qtile = p.causal ? ntq - 1 - L % ntq : L % ntq;
   const int kvh = head / (p.Hq / p.Hkv);
   const int q0 = qtile * QT + wave * 32;
-  const int nt = (p.Skv + KT - 1) / KT;
+  const int nt = tiles_needed(p, qtile * QT, QT);
   const int64_t kvbase = int64_t(kvh) * D;
   const TileAddr ta8 = tile_addr<8>(p, wave_u, ln.lane);      // prologue: all 8 waves load
   const TileAddr ta4 = tile_addr<4>(p, wave_u & 3, ln.lane);  // loop: group A loads
 
+  QBlock A;
+  if (nt == 0) {  // causal: no visible key for any query of the work-group -> 0
+    qblock_init(A, q, p, q0, head, ln, qsign);
+    store_block(A, o, p, q0, head, ln);
+    return;
+  }
   load_tile<NW, false>(k, 0, kb0, p, kvbase, wave_u, ta8);
   load_tile<NW, true>(v, 0, vb0, p, kvbase, wave_u, ta8);
   if (nt > 1) load_tile<NW, false>(k, 1, kb1, p, kvbase, wave_u, ta8);
-  QBlock A;
   qblock_init(A, q, p, q0, head, ln, qsign);
   build_live<NW, KT>(live_tiles, p, nt, wave, ln.lane);
 
@@ -429,7 +463,8 @@ flash_bf16_d128_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   };
   auto valu_part = [&](int t) __attribute__((always_inline)) {
     const uint64_t live = tile_live<KT>(live_tiles, p, t);
-    if (live != ~0ull) mask_scores(A, live, ln);
+    const bool diag = p.causal && int64_t(p.q_offset) + q0 - int64_t(t) * KT < KT - 1;  // wave-uniform
+    if (live != ~0ull || diag) mask_scores(A, live, diag ? causal_rel(p, q0 + ln.n, t) : KT - 1, ln);
     softmax(A, ln);
     rescale(A);
   };
@@ -474,7 +509,7 @@ flash_bf16_d128_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
 }  // namespace
 
 // Launch the fast path. Preconditions (checked by the caller): D == 128,
-// non-causal, q/k/v 16-byte aligned with token strides % 8 == 0, o 4-byte
+// q/k/v 16-byte aligned with token strides % 8 == 0, o 4-byte
 // aligned with o_stride % 2 == 0, Skv * kv_stride * 2 < 2^32.
 hipError_t launch_flash_bf16_d128(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                                   const mx_attn_params& p, hipStream_t s) {

@@ -181,3 +181,58 @@ def test_all_masked_and_deterministic(cuda):
     flash_attn(q, k, v, o1, p); flash_attn(q, k, v, o2, p)
     torch.cuda.synchronize()
     assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+
+
+# Causal / q_offset / GQA on the MFMA path (D = 128, dense aligned strides): the
+# reference's causal rule is key j visible to query row i iff j <= q_offset + i
+# (attention.cu:108, :216-221); rows that see no key produce 0.
+# Sq, Skv, Hq, Hkv, q_offset, masked
+CAUSAL = [
+    (1, 64, 1, 1, 0, False), (300, 300, 4, 4, 0, False), (1000, 1000, 4, 2, 0, False),
+    (513, 1200, 2, 1, 687, False), (700, 700, 2, 2, -100, False), (700, 650, 2, 2, -300, False),
+    (257, 2000, 2, 2, 2 ** 31 - 1, False), (4096, 4096, 8, 8, 0, False), (2048, 2300, 4, 4, 252, True),
+]
+
+
+@pytest.mark.parametrize("case", CAUSAL, ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}x{c[3]}_o{c[4]}{'_m' if c[5] else ''}")
+def test_causal_fast_path(cuda, case):
+    Sq, Skv, Hq, Hkv, off, masked = case
+    print(f"causal case {case}", flush=True)
+    q, k, v, *_ = _make(Sq, Skv, Hq, Hkv, 128, 0, 1.0, 4321 + Sq + Skv, cuda)
+    mask = None
+    if masked:  # text-prefix style padding: 56 of the first 256 keys invalid
+        m = torch.ones(Skv, dtype=torch.uint8)
+        m[torch.randperm(256, generator=torch.Generator().manual_seed(5))[:56]] = 0
+        mask = m
+    p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=128, causal=1, q_offset=off,
+                   kv_valid=None if mask is None else mask.to(cuda))
+    out, buf = _run(flash_attn, q, k, v, p, Sq, Hq * 128)
+    rows = sorted(set(query_rows(Sq, Hq)) | set(range(0, Sq, max(1, Sq // 61))) | {Sq - 1})
+    got = _f32(out[rows])
+    want = oracle.attention_f64(_bits(q), _bits(k), _bits(v), Sq, Skv, Hq, Hkv, 128, 0.0, 1, off,
+                                kv_valid=None if mask is None else mask.numpy(),
+                                rows=np.array(rows, np.int32)).reshape(len(rows), -1)
+    # rows with no visible key are exactly 0
+    dead = [i for i, r in enumerate(rows) if off + r < 0]
+    if dead:
+        assert np.all(got[dead] == 0)
+    ok, err, tol, rr = reference_gate(got, want)
+    assert ok, f"max_abs={err} limit={tol} rel_rms={rr}"
+    live = [i for i, r in enumerate(rows) if off + r >= 0]
+    assert cosine(got[live], want[live]) >= 0.9999 and max_abs(got, want) <= 2e-2
+    _check_guards(buf, 16, Sq, Hq * 128, Hq * 128, rows)
+
+
+def test_causal_equals_truncated_keys(cuda):
+    """Size-independent invariant: row i of causal attention (q_offset = 0) equals
+    non-causal attention of that row over keys 0..i."""
+    S, H = 3000, 4
+    q, k, v, *_ = _make(S, S, H, H, 128, 0, 1.0, 99, cuda)
+    o = torch.empty_like(q)
+    flash_attn(q, k, v, o, AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128, causal=1))
+    for i in (0, 63, 64, 255, 256, 1000, 2999):
+        oi = torch.empty_like(q[i:i + 1])
+        flash_attn(q[i:i + 1].contiguous(), k[: i + 1].contiguous(), v[: i + 1].contiguous(), oi,
+                   AttnParams(Sq=1, Skv=i + 1, Hq=H, Hkv=H, D=128))
+        torch.cuda.synchronize()
+        assert max_abs(_f32(o[i:i + 1]), _f32(oi)) <= 4e-3, i
