@@ -13,7 +13,7 @@
 #include "attn_common.hpp"
 
 namespace mxa {
-hipError_t launch_flash_bf16_d128(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*,
+hipError_t launch_flash_bf16(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*,
                                   const mx_attn_params&, hipStream_t);
 hipError_t launch_naive_attn(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, const mx_attn_params&,
                              hipStream_t);
@@ -106,7 +106,7 @@ int fp8_ok(const void* q, const void* k, const void* v, const void* o, const mx_
 }
 
 bool fast_bf16_ok(const void* q, const void* k, const void* v, const void* o, const mx_attn_params& p) {
-  return p.D == 128 && p.q_stride % 8 == 0 && p.kv_stride % 8 == 0 && p.o_stride % 2 == 0 &&
+  return p.q_stride % 8 == 0 && p.kv_stride % 8 == 0 && p.o_stride % 2 == 0 &&
          aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 4) &&
          (!p.kv_valid || p.Skv <= kMaxMaskedSkv) &&
          int64_t(p.Skv) * p.kv_stride * 2 < (int64_t(1) << 32);  // K/V tiles read through 32-bit buffer offsets
@@ -129,7 +129,7 @@ int mx_flash_attn(const void* q, const void* k, const void* v, void* o, const mx
   auto kk = static_cast<const uint16_t*>(k);
   auto vv = static_cast<const uint16_t*>(v);
   auto oo = static_cast<uint16_t*>(o);
-  if (fast_bf16_ok(q, k, v, o, a)) return hip_status(mxa::launch_flash_bf16_d128(qq, kk, vv, oo, a, s), "flash_attn");
+  if (fast_bf16_ok(q, k, v, o, a)) return hip_status(mxa::launch_flash_bf16(qq, kk, vv, oo, a, s), "flash_attn");
   return hip_status(mxa::launch_naive_attn(qq, kk, vv, oo, a, s), "flash_attn");
 }
 

@@ -1,5 +1,5 @@
-// BF16 flash-attention forward for gfx950 (CDNA4), D = 128, non-causal, with an
-// optional key-padding mask. Reference behaviour: src/kernels/attention.cu:157-290
+// BF16 flash-attention forward for gfx950 (CDNA4), head dim D in {64, 72, 128},
+// optional causal mask with query offset, optional key-padding mask, GQA. Reference behaviour: src/kernels/attention.cu:157-290
 // (flash_kernel), :92-139 (online_softmax), :141-155 (store_output).
 //
 // Design (MI355X-first, not a translation of the reference's mma.sync tiling):
@@ -31,7 +31,6 @@
 //    MFMAs ahead of use.
 //  * Work-groups are remapped so one head's query tiles share an XCD (and its L2).
 #include <type_traits>
-#include <utility>
 #include <utility>
 
 #include "attn_common.hpp"
@@ -68,19 +67,30 @@ extern "C" int mx_debug_timing(void* buf) {
 
 namespace {
 
-constexpr int D = 128;
 constexpr int KT = 64;               // keys per tile
-constexpr int TILEB = KT * D * 2;    // bytes per K (or V) tile
 
-// LDS tile layouts (each 16 KB, filled by 16 DMA ops of 1 KB):
-//  K: [8 d-chunks of 16][64 rows][2 halves of 8 channels]; the 16-byte half is
+// LDS tile layouts (16 KB each at D = 128, filled by DMA ops of 1 KB):
+//  K: [D/16 d-chunks of 16][64 rows][2 halves of 8 channels]; the 16-byte half is
 //     XOR'd with row bit 3 so the 16 rows one ds_read_b128 pass touches land on
 //     16 distinct bank groups. A lane's read address is one per-lane base plus
 //     compile-time offsets (d-chunk * 2048 + key block * 1024).
-//  V: [4 d-blocks of 32][64 rows][64 B]; a ds_read_b64_tr_b16 touches 4 rows x
+//  V: [D/32 d-blocks of 32][64 rows][64 B]; a ds_read_b64_tr_b16 touches 4 rows x
 //     64 B = 256 contiguous bytes per 32 lanes, and its address is again one base
 //     plus compile-time offsets.
 constexpr int K_CHUNK = 2048, V_BLOCK = 4096;
+
+// Per-tile work for head dimension DH. D = 72 runs as 80 in the score MFMA (the
+// K and Q operands' channels 72..79 are zeroed in registers, whatever bytes follow
+// the head in memory) and as 96 in P V (output channels 72..95 are computed from
+// neighbouring bytes and never stored; each output channel depends only on its
+// own V column).
+template <int DH>
+struct Dims {
+  static constexpr int NC = (DH + 15) / 16;          // 16-channel chunks of S = K Q^T
+  static constexpr int NB = (DH + 31) / 32;          // 32-channel blocks of O = P V
+  static constexpr int KOPS = 2 * NC, VOPS = 4 * NB;  // 1 KB DMA ops per K / V tile
+  static constexpr int KTB = NC * K_CHUNK, VTB = NB * V_BLOCK;
+};
 
 // Score-row -> key permutation inside a 32-key block: swap bits 2 and 3.
 __device__ __forceinline__ int perm32(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
@@ -105,34 +115,38 @@ struct Lane {
 };
 
 // Per-wave state of one 32-query block.
+template <int DH>
 struct QBlock {
-  bf16x8 q[8];     // Q^T fragments (MFMA B operand), d-chunk cc: 16 channels
-  f32x16 acc[4];   // O^T, 4 blocks of 32 channels
+  static constexpr int NC = Dims<DH>::NC, NB = Dims<DH>::NB;
+  bf16x8 q[NC];    // Q^T fragments (MFMA B operand), d-chunk cc: 16 channels
+  f32x16 acc[NB];  // O^T, blocks of 32 channels
   f32x16 s[2];     // scores of the current tile, 2 blocks of 32 keys
   bf16x8 p[4];     // P^T (MFMA B operand), 4 chunks of 16 keys
   float m, l, alpha;
 };
 
-__device__ __forceinline__ void qblock_init(QBlock& X, const uint16_t* q, const mx_attn_params& p, int row0,
+template <int DH>
+__device__ __forceinline__ void qblock_init(QBlock<DH>& X, const uint16_t* q, const mx_attn_params& p, int row0,
                                             int head, const Lane& ln, uint32_t qsign) {
   int row = row0 + ln.n;
   row = row < p.Sq ? row : p.Sq - 1;
-  const uint16_t* src = q + int64_t(row) * p.q_stride + head * D + ln.h * 8;
+  const uint16_t* src = q + int64_t(row) * p.q_stride + head * DH + ln.h * 8;
 #pragma unroll
-  for (int cc = 0; cc < 8; ++cc) {
-    u32x4 raw = *reinterpret_cast<const u32x4*>(src + cc * 16);
+  for (int cc = 0; cc < X.NC; ++cc) {
+    u32x4 raw = {0, 0, 0, 0};  // channels past DH (D = 72) stay zero
+    if (DH % 16 == 0 || cc * 16 + ln.h * 8 < DH) raw = *reinterpret_cast<const u32x4*>(src + cc * 16);
     raw ^= qsign;  // negative softmax scale: negate Q (exact) and use |scale|
     X.q[cc] = __builtin_bit_cast(bf16x8, raw);
   }
 #pragma unroll
-  for (int db = 0; db < 4; ++db) X.acc[db] = f32x16{};
+  for (int db = 0; db < X.NB; ++db) X.acc[db] = f32x16{};
   X.m = -__builtin_inff();
   X.l = 0.f;
   X.alpha = 1.f;
 }
 
 // DMA of one 64-key K or V tile: op j writes 1 KB (64 lanes x 16 B) of the LDS
-// layout above; a wave issues 16/NW ops, j = jj*NW + wave. The global side is a
+// layout above; a wave issues ops j = jj*NW + wave (< KOPS or VOPS). The global side is a
 // per-tile buffer resource starting at key t*64 of this KV head: rows at or past
 // Skv fall outside it and load as zeros (no clamping), the per-lane part is a
 // loop-invariant byte offset and the per-op part is wave-uniform, so an op costs
@@ -154,15 +168,18 @@ __device__ __forceinline__ TileAddr tile_addr(const mx_attn_params& p, int wave,
   a.lv = (vrow * kvs + uint32_t((lane & 3) * 8)) * 2u;
   return a;
 }
-template <int NW, bool IS_V>
+template <int NW, bool IS_V, int DH>
 __device__ __forceinline__ void load_tile(const uint16_t* src, int t, unsigned char* dst, const mx_attn_params& p,
                                           int64_t kvbase, int wave, const TileAddr& ta) {
-  constexpr int NLD = 16 / NW;
+  constexpr int NOPS = IS_V ? Dims<DH>::VOPS : Dims<DH>::KOPS;
+  constexpr int NLD = (NOPS + NW - 1) / NW;
   const int key0 = t * KT;
   const __amdgpu_buffer_rsrc_t r =
       buf_rsrc(src + kvbase + int64_t(key0) * p.kv_stride, uint32_t(p.Skv - key0) * uint32_t(p.kv_stride) * 2u);
   auto op = [&](auto jjc) __attribute__((always_inline)) {
     constexpr int jj = decltype(jjc)::value;
+    if constexpr (NOPS % NW != 0)
+      if (jj * NW + wave >= NOPS) return;  // wave-uniform
     MXA_LDS void* d = (MXA_LDS void*)(dst + (jj * NW + wave) * 1024);
     if constexpr (IS_V) {  // d-block j/4 = jj*(NW/4) + wave/4: 64 bytes each
       buf2lds16(r, ta.lv, uint32_t((jj * (NW / 4) + (NW == 8 ? (wave >> 2) : 0)) * 64), d);
@@ -173,26 +190,31 @@ __device__ __forceinline__ void load_tile(const uint16_t* src, int t, unsigned c
   static_for<NLD>(op);
 }
 
-// S^T = K Q^T for one tile (16 MFMA); the first MFMA of each key block takes a
+// S^T = K Q^T for one tile (2 * NC MFMA); the first MFMA of each key block takes a
 // literal zero accumulator (no register initialisation).
-__device__ __forceinline__ void scores(const unsigned char* kd, QBlock& X, const Lane& ln) {
+template <int DH>
+__device__ __forceinline__ void scores(const unsigned char* kd, QBlock<DH>& X, const Lane& ln) {
 #pragma unroll
-  for (int cc = 0; cc < 8; ++cc)
+  for (int cc = 0; cc < X.NC; ++cc)
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(kd + ln.kbase + cc * K_CHUNK + kb * 1024);
+      bf16x8 a = *reinterpret_cast<const bf16x8*>(kd + ln.kbase + cc * K_CHUNK + kb * 1024);
+      // D = 72: the last chunk's upper 8 channels hold whatever follows the head in
+      // memory (possibly NaN padding); zero them so 0 * Q stays 0
+      if (DH % 16 != 0 && cc == X.NC - 1 && ln.h) a = bf16x8{};
       X.s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, X.q[cc], cc == 0 ? f32x16{} : X.s[kb], 0, 0, 0);
     }
 }
 
-// O^T += V^T P^T for one tile (16 MFMA).
-// Key chunk outer, channel block inner: consecutive MFMAs accumulate into four
+// O^T += V^T P^T for one tile (4 * NB MFMA).
+// Key chunk outer, channel block inner: consecutive MFMAs accumulate into
 // different registers, so none waits on the previous one's result.
-__device__ __forceinline__ void pv(const unsigned char* vd, QBlock& X, const Lane& ln) {
+template <int DH>
+__device__ __forceinline__ void pv(const unsigned char* vd, QBlock<DH>& X, const Lane& ln) {
 #pragma unroll
   for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < X.NB; ++db) {
       const unsigned char* va = vd + ln.vbase + db * V_BLOCK + kc * 16 * 64;
       const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MXA_LDS bf16x4*)(va));
       const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MXA_LDS bf16x4*)(va + 4 * 64));
@@ -206,7 +228,8 @@ __device__ __forceinline__ void pv(const unsigned char* vd, QBlock& X, const Lan
 // by 8h once, then every test is a compile-time bit position (no per-lane masks).
 // `rel` is the last key of the tile this lane's query may see (causal; >= 63 when
 // every key is visible), so key index kk is kept iff kk <= rel.
-__device__ __forceinline__ void mask_scores(QBlock& X, uint64_t live, int rel, const Lane& ln) {
+template <int DH>
+__device__ __forceinline__ void mask_scores(QBlock<DH>& X, uint64_t live, int rel, const Lane& ln) {
   const uint64_t lv = live >> (ln.h * 8);
   const uint32_t lo = uint32_t(lv), hi = uint32_t(lv >> 32);
   const int relh = rel - ln.h * 8;
@@ -245,10 +268,9 @@ __device__ __forceinline__ int tiles_needed(const mx_attn_params& p, int qbeg, i
 // a stale max changes nothing but rounding while P stays <= 2^kLazyMax, and the
 // O rescale (alpha != 1) becomes rare instead of happening on most early tiles.
 constexpr float kLazyMax = 8.f;
-__device__ __forceinline__ void softmax(QBlock& X, const Lane& ln) {
+template <int DH>
+__device__ __forceinline__ void softmax(QBlock<DH>& X, const Lane& ln) {
   const float c = ln.c;
-  // four independent max chains (a single wave runs this alone in the ping-pong
-  // schedule, so dependent-issue latency is not hidden by a second wave)
   float mx = X.s[0][0];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
@@ -280,47 +302,52 @@ __device__ __forceinline__ void softmax(QBlock& X, const Lane& ln) {
   }
 }
 
-__device__ __forceinline__ void rescale(QBlock& X) {
+template <int DH>
+__device__ __forceinline__ void rescale(QBlock<DH>& X) {
   if (!__all(X.alpha == 1.f)) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db) X.acc[db] *= X.alpha;
+    for (int db = 0; db < X.NB; ++db) X.acc[db] *= X.alpha;
   }
 }
 
-// Scheduling recipes for one 16-MFMA phase: LDS operand reads kept a few MFMAs
-// ahead of use, and LD vector-memory (LDS-DMA) ops placed one after every
-// fourth MFMA, so no wave issues a burst of DMA ops at once.
-template <int LD>
+// Scheduling recipes for one MFMA phase of NMF MFMAs: LDS operand reads kept a
+// few MFMAs ahead of use, and LD vector-memory (LDS-DMA) ops spread evenly
+// between the MFMAs, so no wave issues a burst of DMA ops at once.
+template <int NMF, int LD>
 __device__ __forceinline__ void sched_k() {
-  __builtin_amdgcn_sched_group_barrier(0x100, MXA_KPF, 0);
+  constexpr int PF = MXA_KPF < NMF ? MXA_KPF : NMF;
+  __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < NMF; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (i % 4 == 1 && i / 4 < LD) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    if (i < 16 - MXA_KPF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if (LD && (i * LD) / NMF != ((i + 1) * LD) / NMF) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    if (i < NMF - PF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
   }
 }
-template <int LD>
+template <int NMF, int LD>
 __device__ __forceinline__ void sched_v() {
-  __builtin_amdgcn_sched_group_barrier(0x100, 2 * MXA_VPF, 0);
+  constexpr int PF = MXA_VPF < NMF ? MXA_VPF : NMF;
+  __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF, 0);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < NMF; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (i % 4 == 1 && i / 4 < LD) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    if (i < 16 - MXA_VPF) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    if (LD && (i * LD) / NMF != ((i + 1) * LD) / NMF) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    if (i < NMF - PF) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
   }
 }
 
-__device__ __forceinline__ void store_block(const QBlock& X, uint16_t* o, const mx_attn_params& p, int row0,
+template <int DH>
+__device__ __forceinline__ void store_block(const QBlock<DH>& X, uint16_t* o, const mx_attn_params& p, int row0,
                                             int head, const Lane& ln) {
   const int row = row0 + ln.n;
   if (row >= p.Sq) return;
   const float inv = X.l > 0.f ? 1.f / X.l : 0.f;
-  uint16_t* dst = o + int64_t(row) * p.o_stride + head * D + ln.h * 4;
+  uint16_t* dst = o + int64_t(row) * p.o_stride + head * DH + ln.h * 4;
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < X.NB; ++db)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
+      if (DH % 32 != 0 && db * 32 + g * 8 >= DH) continue;  // D = 72: channels 72..95 are not output
       uint32_t* d32 = reinterpret_cast<uint32_t*>(dst + db * 32 + g * 8);
       d32[0] = pack_bf16x2(X.acc[db][g * 4] * inv, X.acc[db][g * 4 + 1] * inv);
       d32[1] = pack_bf16x2(X.acc[db][g * 4 + 2] * inv, X.acc[db][g * 4 + 3] * inv);
@@ -333,12 +360,15 @@ __device__ __forceinline__ void store_block(const QBlock& X, uint16_t* o, const 
 // lives in stage t % 2 and the loads of tile t + 1 (clamped to the last tile,
 // so the ops are unconditional and interleave with the MFMAs) go into the
 // stage tile t - 1 used.
+template <int DH>
 __global__ void __launch_bounds__(512, 1)
-flash_bf16_d128_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                   uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign) {
-  constexpr int NW = 8, QT = NW * 32, OPS = 2 * (16 / NW);
-  __shared__ __align__(16) unsigned char st0[2 * TILEB];
-  __shared__ __align__(16) unsigned char st1[2 * TILEB];
+flash_bf16_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+              uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign) {
+  using Dm = Dims<DH>;
+  constexpr int NW = 8, QT = NW * 32;
+  constexpr int OPS = (Dm::KOPS + NW - 1) / NW + (Dm::VOPS + NW - 1) / NW;  // DMA ops per wave per tile
+  __shared__ __align__(16) unsigned char st0[Dm::KTB + Dm::VTB];
+  __shared__ __align__(16) unsigned char st1[Dm::KTB + Dm::VTB];
   __shared__ uint64_t live_tiles[kMaxLiveTiles];
   MXA_CLOCK_BEGIN
   const Lane ln(c);
@@ -351,18 +381,18 @@ flash_bf16_d128_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   const int kvh = head / (p.Hq / p.Hkv);
   const int q0 = qtile * QT + wave * 32;
   const int nt = tiles_needed(p, qtile * QT, QT);
-  const int64_t kvbase = int64_t(kvh) * D;
+  const int64_t kvbase = int64_t(kvh) * DH;
   const TileAddr ta = tile_addr<NW>(p, wave_u, ln.lane);
 
-  QBlock A;
+  QBlock<DH> A;
   qblock_init(A, q, p, q0, head, ln, qsign);
   if (nt == 0) {  // causal: no visible key for any query of the work-group -> 0
     store_block(A, o, p, q0, head, ln);
     return;
   }
   auto issue = [&](int t, unsigned char* dst) __attribute__((always_inline)) {
-    load_tile<NW, false>(k, t, dst, p, kvbase, wave_u, ta);
-    load_tile<NW, true>(v, t, dst + TILEB, p, kvbase, wave_u, ta);
+    load_tile<NW, false, DH>(k, t, dst, p, kvbase, wave_u, ta);
+    load_tile<NW, true, DH>(v, t, dst + Dm::KTB, p, kvbase, wave_u, ta);
   };
   issue(0, st0);
   build_live<NW, KT>(live_tiles, p, nt, wave, ln.lane);
@@ -374,13 +404,13 @@ flash_bf16_d128_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
     const uint64_t live = tile_live<KT>(live_tiles, p, t);
     issue(t + 1 < nt ? t + 1 : nt - 1, nxt);
     scores(cur, A, ln);
-    sched_k<OPS>();
+    sched_k<2 * Dm::NC, OPS>();
     const bool diag = p.causal && int64_t(p.q_offset) + q0 - int64_t(t) * KT < KT - 1;  // wave-uniform
     if (live != ~0ull || diag) mask_scores(A, live, diag ? causal_rel(p, q0 + ln.n, t) : KT - 1, ln);
     softmax(A, ln);
     rescale(A);
-    pv(cur + TILEB, A, ln);
-    sched_v<0>();
+    pv(cur + Dm::KTB, A, ln);
+    sched_v<4 * Dm::NB, 0>();
   };
   for (int t = 0; t < nt; t += 2) {
     step(t, st0, st1);
@@ -403,14 +433,17 @@ flash_bf16_d128_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
 // K(t+2) and V(t+1) go into the buffers of K(t) and V(t-1), both last read in
 // period 2t; group A issues all of their DMA ops during its MFMA period 2t+1
 // (8 per wave, one per four MFMAs), and waits for them at the top of tile t+1.
+template <int DH>
 __global__ void __launch_bounds__(512, 1)
-flash_bf16_d128_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                   uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign) {
+flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+              uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign) {
+  using Dm = Dims<DH>;
   constexpr int NW = 8, QT = NW * 32;
-  __shared__ __align__(16) unsigned char kb0[TILEB];
-  __shared__ __align__(16) unsigned char kb1[TILEB];
-  __shared__ __align__(16) unsigned char vb0[TILEB];
-  __shared__ __align__(16) unsigned char vb1[TILEB];
+  constexpr int LDK = (Dm::KOPS + 3) / 4, LDV = (Dm::VOPS + 3) / 4;  // loop DMA ops per group-A wave
+  __shared__ __align__(16) unsigned char kb0[Dm::KTB];
+  __shared__ __align__(16) unsigned char kb1[Dm::KTB];
+  __shared__ __align__(16) unsigned char vb0[Dm::VTB];
+  __shared__ __align__(16) unsigned char vb1[Dm::VTB];
   __shared__ uint64_t live_tiles[kMaxLiveTiles];
   MXA_CLOCK_BEGIN
   const Lane ln(c);
@@ -424,19 +457,19 @@ flash_bf16_d128_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   const int kvh = head / (p.Hq / p.Hkv);
   const int q0 = qtile * QT + wave * 32;
   const int nt = tiles_needed(p, qtile * QT, QT);
-  const int64_t kvbase = int64_t(kvh) * D;
+  const int64_t kvbase = int64_t(kvh) * DH;
   const TileAddr ta8 = tile_addr<8>(p, wave_u, ln.lane);      // prologue: all 8 waves load
   const TileAddr ta4 = tile_addr<4>(p, wave_u & 3, ln.lane);  // loop: group A loads
 
-  QBlock A;
+  QBlock<DH> A;
   if (nt == 0) {  // causal: no visible key for any query of the work-group -> 0
     qblock_init(A, q, p, q0, head, ln, qsign);
     store_block(A, o, p, q0, head, ln);
     return;
   }
-  load_tile<NW, false>(k, 0, kb0, p, kvbase, wave_u, ta8);
-  load_tile<NW, true>(v, 0, vb0, p, kvbase, wave_u, ta8);
-  if (nt > 1) load_tile<NW, false>(k, 1, kb1, p, kvbase, wave_u, ta8);
+  load_tile<NW, false, DH>(k, 0, kb0, p, kvbase, wave_u, ta8);
+  load_tile<NW, true, DH>(v, 0, vb0, p, kvbase, wave_u, ta8);
+  if (nt > 1) load_tile<NW, false, DH>(k, 1, kb1, p, kvbase, wave_u, ta8);
   qblock_init(A, q, p, q0, head, ln, qsign);
   build_live<NW, KT>(live_tiles, p, nt, wave, ln.lane);
 
@@ -447,17 +480,17 @@ flash_bf16_d128_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
                        unsigned char* vfree, auto load) __attribute__((always_inline)) {
     __builtin_amdgcn_s_setprio(1);
     if constexpr (decltype(load)::value) {
-      load_tile<4, true>(v, t + 1 < nt ? t + 1 : nt - 1, vfree, p, kvbase, wave_u & 3, ta4);
+      load_tile<4, true, DH>(v, t + 1 < nt ? t + 1 : nt - 1, vfree, p, kvbase, wave_u & 3, ta4);
       pv(vcur, A, ln);
-      sched_v<4>();
-      load_tile<4, false>(k, t + 2 < nt ? t + 2 : nt - 1, kfree, p, kvbase, wave_u & 3, ta4);
+      sched_v<4 * Dm::NB, LDV>();
+      load_tile<4, false, DH>(k, t + 2 < nt ? t + 2 : nt - 1, kfree, p, kvbase, wave_u & 3, ta4);
       scores(kc1, A, ln);
-      sched_k<4>();
+      sched_k<2 * Dm::NC, LDK>();
     } else {
       pv(vcur, A, ln);
-      sched_v<0>();
+      sched_v<4 * Dm::NB, 0>();
       scores(kc1, A, ln);
-      sched_k<0>();
+      sched_k<2 * Dm::NC, 0>();
     }
     __builtin_amdgcn_s_setprio(0);
   };
@@ -473,14 +506,14 @@ flash_bf16_d128_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   __syncthreads();  // K(0), V(0), K(1) and the liveness bitmaps are visible
   if (group_a) {    // period -1: S_A(0)
     scores(kb0, A, ln);
-    sched_k<0>();
+    sched_k<2 * Dm::NC, 0>();
   }
   block_sync();
   if (group_a) {    // period 0: A softmax(0), B S_B(0)
     valu_part(0);
   } else {
     scores(kb0, A, ln);
-    sched_k<0>();
+    sched_k<2 * Dm::NC, 0>();
   }
 
   // Tile t: kc1 = K(t+1), vcur = V(t); kfree / vfree receive K(t+2) / V(t+1).
@@ -508,22 +541,30 @@ flash_bf16_d128_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
 
 }  // namespace
 
-// Launch the fast path. Preconditions (checked by the caller): D == 128,
-// q/k/v 16-byte aligned with token strides % 8 == 0, o 4-byte
-// aligned with o_stride % 2 == 0, Skv * kv_stride * 2 < 2^32.
-hipError_t launch_flash_bf16_d128(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
-                                  const mx_attn_params& p, hipStream_t s) {
+// Launch the fast path. Preconditions (checked by the caller): D in {64, 72, 128},
+// q/k/v 16-byte aligned with token strides % 8 == 0, o 4-byte aligned with
+// o_stride % 2 == 0, Skv * kv_stride * 2 < 2^32.
+hipError_t launch_flash_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
+                             const mx_attn_params& p, hipStream_t s) {
   const float c = __builtin_fabsf(p.scale) * kLog2e;
   const uint32_t qsign = p.scale < 0.f ? 0x80008000u : 0u;
   constexpr int QT = 256;  // both shapes cover 256 queries per work-group
   const int ntq = (p.Sq + QT - 1) / QT;
   const int64_t blocks = int64_t(ntq) * p.Hq;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-#if MXA_BF16_KIND == 9
-  hipLaunchKernelGGL(flash_bf16_d128_pp, dim3(unsigned(blocks)), dim3(512), 0, s, q, k, v, o, p, c, qsign);
+  const dim3 grid{unsigned(blocks)}, block{512};
+  switch (p.D) {
+    case 128:
+#if MXA_BF16_KIND == 8
+      hipLaunchKernelGGL(flash_bf16_w8<128>, grid, block, 0, s, q, k, v, o, p, c, qsign);
 #else
-  hipLaunchKernelGGL(flash_bf16_d128_w8, dim3(unsigned(blocks)), dim3(512), 0, s, q, k, v, o, p, c, qsign);
+      hipLaunchKernelGGL(flash_bf16_pp<128>, grid, block, 0, s, q, k, v, o, p, c, qsign);
 #endif
+      break;
+    case 64: hipLaunchKernelGGL(flash_bf16_pp<64>, grid, block, 0, s, q, k, v, o, p, c, qsign); break;
+    case 72: hipLaunchKernelGGL(flash_bf16_pp<72>, grid, block, 0, s, q, k, v, o, p, c, qsign); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -236,3 +236,44 @@ def test_causal_equals_truncated_keys(cuda):
                    AttnParams(Sq=1, Skv=i + 1, Hq=H, Hkv=H, D=128))
         torch.cuda.synchronize()
         assert max_abs(_f32(o[i:i + 1]), _f32(oi)) <= 4e-3, i
+
+
+# D = 64 and D = 72 on the MFMA path, with NaN in the stride padding after each
+# token's heads (D = 72 reads past the head in 16-byte chunks and must ignore it).
+# Sq, Skv, Hq, Hkv, D, causal, q_offset, masked
+SMALL_D = [
+    (1000, 1000, 4, 2, 64, 0, 0, False), (1000, 1000, 4, 2, 72, 0, 0, False),
+    (777, 1200, 6, 3, 72, 1, 423, False), (513, 513, 2, 2, 64, 1, 0, True),
+    (2048, 2048, 8, 8, 72, 0, 0, True), (70, 4000, 3, 1, 72, 1, 3930, False),
+]
+
+
+@pytest.mark.parametrize("case", SMALL_D, ids=lambda c: "x".join(map(str, c[:5])) + f"_c{c[5]}o{c[6]}{'_m' if c[7] else ''}")
+def test_small_head_dim_fast_path(cuda, case):
+    Sq, Skv, Hq, Hkv, D, causal, off, masked = case
+    print(f"small-D case {case}", flush=True)
+    g = torch.Generator(device=cuda); g.manual_seed(777 + Sq + D)
+    qs, ks = Hq * D + 8, Hkv * D + 8  # strides % 8 == 0: the fast path
+    q = torch.randn(Sq, qs, generator=g, device=cuda).to(torch.bfloat16)
+    k = torch.randn(Skv, ks, generator=g, device=cuda).to(torch.bfloat16)
+    v = torch.randn(Skv, ks, generator=g, device=cuda).to(torch.bfloat16)
+    for t, h in ((q, Hq), (k, Hkv), (v, Hkv)):
+        t[:, h * D:] = float("nan")
+    mask = None
+    if masked:
+        m = torch.ones(Skv, dtype=torch.uint8)
+        m[torch.randperm(Skv, generator=torch.Generator().manual_seed(9))[: Skv // 5]] = 0
+        mask = m
+    p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=D, causal=causal, q_offset=off, q_stride=qs, kv_stride=ks,
+                   o_stride=Hq * D, kv_valid=None if mask is None else mask.to(cuda))
+    out, buf = _run(flash_attn, q, k, v, p, Sq, Hq * D)
+    rows = sorted(set(query_rows(Sq, Hq)) | set(range(0, Sq, max(1, Sq // 41))) | {Sq - 1})
+    got = _f32(out[rows])
+    assert np.all(np.isfinite(got))
+    want = oracle.attention_f64(_bits(q), _bits(k), _bits(v), Sq, Skv, Hq, Hkv, D, 0.0, causal, off,
+                                q_stride=qs, kv_stride=ks, kv_valid=None if mask is None else mask.numpy(),
+                                rows=np.array(rows, np.int32)).reshape(len(rows), -1)
+    ok, err, tol, rr = reference_gate(got, want)
+    assert ok, f"max_abs={err} limit={tol} rel_rms={rr}"
+    assert cosine(got, want) >= 0.9999 and max_abs(got, want) <= 2e-2
+    _check_guards(buf, 16, Sq, Hq * D, Hq * D, rows)
