@@ -104,6 +104,19 @@ const char* mx_last_error(void);
 /* Library build identifier (kernel variant string). */
 const char* mx_version(void);
 
+/* Reference: mx::head_norm_rope, src/kernels/ops.h:37-41 (impl ops.cu:87-119, :197-210),
+ * the step that feeds attention in every DiT block: for each token s < S and head
+ * h < H, x = in[s*in_stride + col0 + h*D .. +D) (bf16); if norm_w, x = x * rsqrt(
+ * mean(x^2) + eps) * norm_w (per-head RMS-norm; the sum of squares follows the
+ * reference's reduction order); then rotary embedding of the first `rot` channels
+ * with cos/sin [S, rot/2] (fp32), MX_ROPE_INTERLEAVED pairing (2i, 2i+1) or
+ * MX_ROPE_HALF pairing (i, i + rot/2); out[(s*H + h)*D + d] = bf16(x). Rules of
+ * the reference's MX_CHECK: D even, D <= 256, rot even, rot <= D; S <= 0 is a no-op.
+ * Results match the reference to bf16 rounding (its rsqrtf is an approximation). */
+enum { MX_ROPE_NONE = 0, MX_ROPE_INTERLEAVED = 1, MX_ROPE_HALF = 2 };
+int mx_head_norm_rope(const void* in, int64_t S, int64_t in_stride, int64_t col0, int H, int D, const float* norm_w,
+                      float eps, const float* cos, const float* sin, int rot, int mode, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,7 +19,7 @@ MX_OK, MX_E_INVALID, MX_E_HIP, MX_E_UNSUPPORTED = 0, -1, -2, -3
 SYMBOLS = (
     "mx_flash_attn", "mx_flash_attn_fp8_workspace", "mx_flash_attn_fp8_supported",
     "mx_flash_attn_fp8_ok", "mx_flash_attn_fp8", "mx_attn_reference", "mx_sage_layout_of",
-    "mx_sage_quantize", "mx_sage_attend", "mx_last_error", "mx_version",
+    "mx_sage_quantize", "mx_sage_attend", "mx_last_error", "mx_version", "mx_head_norm_rope",
 )
 
 
@@ -62,6 +62,8 @@ def load():
         "mx_sage_attend": ([vp, P, vp, vp], ctypes.c_int),
         "mx_last_error": ([], ctypes.c_char_p),
         "mx_version": ([], ctypes.c_char_p),
+        "mx_head_norm_rope": ([vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, vp,
+                               ctypes.c_float, vp, vp, ctypes.c_int, ctypes.c_int, vp, vp], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

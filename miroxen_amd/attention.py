@@ -119,5 +119,18 @@ def sage_attend(o, p: AttnParams, ws, stream=None) -> None:
     _lib.check(_lib.load().mx_sage_attend(_addr(o), ctypes.byref(c), _addr(ws), _stream(stream)))
 
 
+ROPE_NONE, ROPE_INTERLEAVED, ROPE_HALF = 0, 1, 2  # reference RopeMode, src/kernels/ops.h:35
+
+
+def head_norm_rope(inp, S: int, in_stride: int, col0: int, H: int, D: int, norm_w, eps: float, cos, sin,
+                   rot: int, mode: int, out, stream=None) -> None:
+    """Reference mx::head_norm_rope (src/kernels/ops.h:37-41, ops.cu:197-210): per-head
+    RMS-norm (norm_w fp32 [D] or None) then RoPE of the first `rot` channels with
+    cos/sin fp32 [S, rot/2]; reads in[s*in_stride + col0 + h*D + d], writes dense
+    out [S, H, D] bf16."""
+    _lib.check(_lib.load().mx_head_norm_rope(_addr(inp), S, in_stride, col0, H, D, _addr(norm_w), eps,
+                                             _addr(cos), _addr(sin), rot, mode, _addr(out), _stream(stream)))
+
+
 def version() -> str:
     return _lib.load().mx_version().decode()

@@ -11,8 +11,11 @@
 #include <limits>
 
 #include "attn_common.hpp"
+#include "norm_rope.hpp"
 
 namespace mxa {
+hipError_t launch_head_norm_rope(const uint16_t*, int64_t, int64_t, int64_t, int, int, const NormRope&, uint16_t*,
+                                 hipStream_t);
 hipError_t launch_flash_bf16(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*,
                                   const mx_attn_params&, hipStream_t);
 hipError_t launch_naive_attn(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, const mx_attn_params&,
@@ -229,6 +232,24 @@ int mx_sage_attend(void* o, const mx_attn_params* p, const void* ws, void* strea
   return hip_status(mxa::launch_sage_attend(static_cast<uint16_t*>(o), a, static_cast<const char*>(ws),
                                             static_cast<hipStream_t>(stream)),
                     "sage_attend");
+}
+
+int mx_head_norm_rope(const void* in, int64_t S, int64_t in_stride, int64_t col0, int H, int D, const float* norm_w,
+                      float eps, const float* cos, const float* sin, int rot, int mode, void* out, void* stream) {
+  if (S <= 0) return MX_OK;  // reference ops.cu:200
+  // reference MX_CHECK, ops.cu:201
+  if (!(D % 2 == 0 && D > 0 && D <= 256 && rot >= 0 && rot <= D && rot % 2 == 0))
+    return fail(MX_E_INVALID, "head_norm_rope: D=%d rot=%d", D, rot);
+  if (!(mode == MX_ROPE_NONE || mode == MX_ROPE_INTERLEAVED || mode == MX_ROPE_HALF))
+    return fail(MX_E_INVALID, "head_norm_rope: unknown rope mode %d", mode);
+  if (!in || !out || H <= 0 || in_stride < col0 + int64_t(H) * D || col0 < 0)
+    return fail(MX_E_INVALID, "head_norm_rope: bad tensor arguments");
+  if (mode != MX_ROPE_NONE && rot > 0 && (!cos || !sin))
+    return fail(MX_E_INVALID, "head_norm_rope: rope needs cos and sin tables");
+  const mxa::NormRope nr{norm_w, eps, cos, sin, rot, mode};
+  return hip_status(mxa::launch_head_norm_rope(static_cast<const uint16_t*>(in), S, in_stride, col0, H, D, nr,
+                                               static_cast<uint16_t*>(out), static_cast<hipStream_t>(stream)),
+                    "head_norm_rope");
 }
 
 }  // extern "C"

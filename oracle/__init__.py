@@ -57,6 +57,8 @@ def lib():
         L.or_sage_emulate.restype = None
         L.or_sage_emulate.argtypes = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64,
                                       _p, _p, _i, _p, _i, _f]
+        L.or_head_norm_rope.restype = None
+        L.or_head_norm_rope.argtypes = [_p, _i64, _i64, _i64, _i, _i, _p, _f, _p, _p, _i, _i, _p]
         L.or_num_threads.restype = _i
         _lib = L
     return _lib
@@ -169,3 +171,15 @@ def sage_reference(q, k, v, Sq, Skv, Hq, Hkv, D, scale=0.0, q_stride=0, kv_strid
 
 def num_threads() -> int:
     return int(lib().or_num_threads())
+
+
+def head_norm_rope(inp, S, in_stride, col0, H, D, norm_w=None, eps=0.0, cos=None, sin=None, rot=0, mode=0):
+    """Reference head_norm_rope (ops.cu:87-119) -> bf16 bits [S, H, D]."""
+    inp = _c(inp, np.uint16)
+    nw = None if norm_w is None else _c(norm_w, np.float32)
+    cs = None if cos is None else _c(cos, np.float32)
+    sn = None if sin is None else _c(sin, np.float32)
+    out = np.zeros((S, H, D), np.uint16)
+    lib().or_head_norm_rope(_ptr(inp), S, in_stride, col0, H, D, _ptr(nw), float(eps), _ptr(cs), _ptr(sn),
+                            rot, mode, _ptr(out))
+    return out

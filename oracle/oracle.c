@@ -18,6 +18,11 @@
  *    independent numpy restatement on random data.
  *  - or_e4m3: pinned by the OCP FP8 table (all 256 codes decode/encode round
  *    trip, half-way cases, saturation to 448, subnormals).
+ *  - or_head_norm_rope: pinned by numpy closed forms (RMS-norm in float64, RoPE
+ *    as complex multiplication), invariants (rotation preserves pair norms,
+ *    rot = 0 and no norm is the identity, half mode = interleaved mode on
+ *    permuted channels) and the butterfly order checked against a direct
+ *    restatement of the reference's shuffle pattern.
  *  - or_sage_emulate: pinned by its limit: with exact (unquantized) P/V it must
  *    equal or_attention_f64 to fp32 accuracy, and by the reference gate
  *    (rel-RMS < 4 % vs exact attention, tests/attention_fp8_test.cpp:65).
@@ -318,6 +323,70 @@ void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, cons
       o[d] = acc[d] * vamax[kvh * D + d] * inv;
     }
     free(acc);
+  }
+}
+
+/* ---------- head_norm_rope (reference src/kernels/ops.cu:87-119, :14-29) ----------
+ * Per (token s, head h): x_d = bf16 in[s*in_stride + col0 + h*D + d]. If norm_w:
+ * ss = the reference block_sum of x_d^2 over threads d < ceil(D/32)*32 (zeros
+ * past D): inside each 32-thread warp an xor butterfly (offsets 16, 8, 4, 2, 1),
+ * then the same butterfly over the warp partials padded to 32 slots;
+ * x_d = x_d * rstd * norm_w[d] with rstd = 1/sqrt(ss/D + eps) (the reference
+ * calls rsqrtf, an approximation; here the correctly rounded value). Then RoPE of
+ * channels d < rot (mode 1: pairs (2i, 2i+1); mode 2: (i, i + rot/2)):
+ * (a, b) -> (a c - b s, a s + b c) with c, s = cos/sin[s][pair]; output bf16. */
+static float or_butterfly32(const float* x) { /* x[32] -> the xor-butterfly total */
+  float a[32];
+  memcpy(a, x, sizeof a);
+  for (int o = 16; o > 0; o >>= 1) {
+    float b[32];
+    for (int l = 0; l < 32; ++l) b[l] = a[l] + a[l ^ o];
+    memcpy(a, b, sizeof a);
+  }
+  return a[0];
+}
+
+void or_head_norm_rope(const uint16_t* in, int64_t S, int64_t in_stride, int64_t col0, int H, int D,
+                       const float* norm_w, float eps, const float* cs, const float* sn, int rot, int mode,
+                       uint16_t* out) {
+  const int nwarp = (D + 31) / 32, half = rot / 2;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < S * H; ++r) {
+    const int64_t s = r / H;
+    const int h = (int)(r % H);
+    float v[256], buf[256];
+    for (int d = 0; d < nwarp * 32; ++d)
+      v[d] = d < D ? or_bf16_to_f32(in[s * in_stride + col0 + (int64_t)h * D + d]) : 0.f;
+    if (norm_w) {
+      float part[32] = {0};
+      for (int w = 0; w < nwarp; ++w) {
+        float sq[32];
+        for (int l = 0; l < 32; ++l) sq[l] = v[w * 32 + l] * v[w * 32 + l];
+        part[w] = or_butterfly32(sq);
+      }
+      const float ss = or_butterfly32(part);
+      const float rstd = (float)(1.0 / sqrt((double)(ss / (float)D + eps)));
+      for (int d = 0; d < D; ++d) v[d] = v[d] * rstd * norm_w[d];
+    }
+    for (int d = 0; d < D; ++d) buf[d] = v[d];
+    if (mode != 0 && rot > 0) {
+      for (int d = 0; d < rot; ++d) {
+        int pair, idx;
+        float other;
+        if (mode == 1) {
+          pair = d >> 1;
+          idx = d & 1;
+          other = buf[d ^ 1];
+        } else {
+          pair = d < half ? d : d - half;
+          idx = d < half ? 0 : 1;
+          other = buf[d < half ? d + half : d - half];
+        }
+        const float c = cs[s * half + pair], si = sn[s * half + pair];
+        v[d] = idx == 0 ? v[d] * c - other * si : other * si + v[d] * c;
+      }
+    }
+    for (int d = 0; d < D; ++d) out[r * D + d] = or_f32_to_bf16(v[d]);
   }
 }
 

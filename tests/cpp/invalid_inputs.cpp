@@ -7,6 +7,7 @@
 #include <stdexcept>
 
 #include "miroxen/attention.h"
+#include "miroxen/head_norm_rope.h"
 
 using namespace mx;
 
@@ -43,10 +44,18 @@ int main() {
   } catch (const std::runtime_error& e) {
     ++rejected;
   }
+  // head_norm_rope: the reference's MX_CHECK (ops.cu:201) rejects an odd D
+  int nr_rejected = 0;
+  try {
+    head_norm_rope(b, 4, 256, 0, 2, 127, nullptr, 0.f, nullptr, nullptr, 0, ROPE_NONE, b, nullptr);
+  } catch (const std::runtime_error&) {
+    ++nr_rejected;
+  }
   // the workspace query is pure host arithmetic
   AttnParams c2;
   c2.Sq = 4352; c2.Skv = 4352; c2.Hq = 24; c2.Hkv = 24; c2.D = 128;
   const size_t ws = flash_attn_fp8_workspace(c2);
-  std::printf("invalid input checks: %d rejected; config-2 workspace %zu bytes\n", rejected, ws);
-  return rejected == 23 && ws > 0 ? 0 : 1;
+  std::printf("invalid input checks: %d rejected; head_norm_rope %d rejected; config-2 workspace %zu bytes\n",
+              rejected, nr_rejected, ws);
+  return rejected == 23 && nr_rejected == 1 && ws > 0 ? 0 : 1;
 }

@@ -109,3 +109,15 @@ def test_cpp_dropin_header_rejects_invalid_inputs(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "23 rejected" in r.stdout
+
+
+@pytest.mark.parametrize("bad", [dict(D=7), dict(D=258), dict(rot=130), dict(rot=3), dict(mode=3),
+                                 dict(cos=0), dict(H=0), dict(col0=-1)])
+def test_head_norm_rope_rejects(bad):
+    """Reference MX_CHECK (src/kernels/ops.cu:201) plus null/shape checks, host-side."""
+    from miroxen_amd import head_norm_rope
+    a = dict(S=4, in_stride=256, col0=0, H=2, D=128, rot=128, mode=1, cos=256, sin=256)
+    a.update(bad)
+    with pytest.raises(RuntimeError):
+        head_norm_rope(256, a["S"], a["in_stride"], a["col0"], a["H"], a["D"], None, 1e-6, a["cos"], a["sin"],
+                       a["rot"], a["mode"], 512, stream=0)

@@ -294,3 +294,111 @@ def test_sage_lazy_max_headroom_matches_reference_rule():
     assert rel_rms(lazy, exact) <= 1.1 * rel_rms(exact_rule, exact) + 1e-3
     assert rel_rms(lazy, exact) < 0.04 and cosine(lazy, exact) > 0.995
     assert cosine(lazy, exact_rule) > 0.999
+
+
+# ---------------- head_norm_rope (reference src/kernels/ops.cu:87-119) ----------------
+
+def _nr_inputs(S, H, D, seed, stride_extra=0, col0=0):
+    rng = np.random.default_rng(seed)
+    stride = col0 + H * D + stride_extra
+    x = oracle.f32_to_bf16((rng.standard_normal((S, stride)) * 1.7).astype(np.float32))
+    return x, stride
+
+
+def _ulps(a, b):
+    """bf16 ulp distance of two bf16 bit arrays (same sign assumed for non-zero)."""
+    fa, fb = oracle.bf16_to_f32(a).astype(np.float64), oracle.bf16_to_f32(b).astype(np.float64)
+    ulp = np.maximum(np.abs(fb), 1e-30) * 2.0 ** -7
+    return np.abs(fa - fb) / ulp
+
+
+def test_head_norm_rope_identity():
+    """No norm and rot = 0: a strided gather, bit-exact."""
+    S, H, D, col0 = 5, 3, 72, 16
+    x, stride = _nr_inputs(S, H, D, 1, stride_extra=8, col0=col0)
+    out = oracle.head_norm_rope(x, S, stride, col0, H, D)
+    want = x[:, col0:col0 + H * D].reshape(S, H, D)
+    assert np.array_equal(out, want)
+
+
+@pytest.mark.parametrize("D", [64, 72, 128, 256])
+def test_head_norm_rope_norm_matches_float64(D):
+    S, H = 7, 2
+    x, stride = _nr_inputs(S, H, D, D)
+    w = np.random.default_rng(3).uniform(0.5, 1.5, D).astype(np.float32)
+    eps = 1e-6
+    out = oracle.head_norm_rope(x, S, stride, 0, H, D, norm_w=w, eps=eps)
+    xf = oracle.bf16_to_f32(x).astype(np.float64).reshape(S, H, D)
+    want = xf / np.sqrt((xf ** 2).mean(-1, keepdims=True) + eps) * w
+    got = oracle.bf16_to_f32(out).astype(np.float64)
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-3)) <= 2.0 ** -7  # within bf16 rounding
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_head_norm_rope_rope_is_complex_rotation(mode):
+    S, H, D, rot = 6, 2, 128, 96
+    x, stride = _nr_inputs(S, H, D, 11)
+    rng = np.random.default_rng(5)
+    ang = rng.uniform(-np.pi, np.pi, (S, rot // 2))
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    out = oracle.bf16_to_f32(oracle.head_norm_rope(x, S, stride, 0, H, D, cos=cs, sin=sn, rot=rot, mode=mode))
+    xf = oracle.bf16_to_f32(x).astype(np.float64).reshape(S, H, D)
+    half = rot // 2
+    if mode == 1:
+        a, b = xf[..., 0:rot:2], xf[..., 1:rot:2]
+    else:
+        a, b = xf[..., :half], xf[..., half:rot]
+    z = (a + 1j * b) * np.exp(1j * ang.astype(np.float64))[:, None, :]
+    if mode == 1:
+        ga, gb = out[..., 0:rot:2], out[..., 1:rot:2]
+    else:
+        ga, gb = out[..., :half], out[..., half:rot]
+    tol = 2.0 ** -8 * (np.abs(z) + 1e-3)
+    assert np.all(np.abs(ga - z.real) <= tol) and np.all(np.abs(gb - z.imag) <= tol)
+    assert np.array_equal(out[..., rot:], xf[..., rot:].astype(np.float32))  # untouched tail
+
+
+def test_head_norm_rope_half_equals_permuted_interleaved():
+    """ROPE_HALF on channels (i, i+rot/2) == ROPE_INTERLEAVED on the same values laid out
+    as (2i, 2i+1), bit for bit (no norm: the rotation alone)."""
+    S, H, D = 4, 3, 64
+    x, stride = _nr_inputs(S, H, D, 21)
+    ang = np.random.default_rng(8).uniform(-3, 3, (S, D // 2))
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    perm = np.empty(D, np.int64)
+    perm[0::2], perm[1::2] = np.arange(D // 2), np.arange(D // 2, D)
+    xi = x.reshape(S, H, D)[..., perm].reshape(S, H * D)
+    half = oracle.head_norm_rope(x, S, stride, 0, H, D, cos=cs, sin=sn, rot=D, mode=2)
+    inter = oracle.head_norm_rope(xi, S, H * D, 0, H, D, cos=cs, sin=sn, rot=D, mode=1)
+    assert np.array_equal(inter, half[..., perm])
+
+
+def _shfl_xor_block_sum(vals, D):
+    """The reference's block_sum (ops.cu:14-29) simulated lane by lane in float32:
+    __shfl_xor_sync butterflies within 32-thread warps, then over the warp partials."""
+    nthreads = (D + 31) // 32 * 32
+    v = np.zeros(nthreads, np.float32); v[:D] = vals
+    for o in (16, 8, 4, 2, 1):
+        v = (v + v[np.arange(nthreads) ^ o]).astype(np.float32)
+    sh = np.zeros(32, np.float32); sh[: nthreads // 32] = v[::32]
+    for o in (16, 8, 4, 2, 1):
+        sh = (sh + sh[np.arange(32) ^ o]).astype(np.float32)
+    return sh[0]
+
+
+@pytest.mark.parametrize("D", [64, 72, 128, 200])
+def test_head_norm_rope_sum_order_is_the_reference_shuffle_pattern(D):
+    """Inputs whose squares span many binades, so the association order shows in the
+    float32 sum: the oracle's rstd must come from the shuffle-pattern sum."""
+    S, H = 3, 1
+    rng = np.random.default_rng(D)
+    xf = (rng.standard_normal((S, D)) * np.exp2(rng.integers(-12, 12, (S, D)))).astype(np.float32)
+    x = oracle.f32_to_bf16(xf)
+    w = np.ones(D, np.float32)
+    out = oracle.bf16_to_f32(oracle.head_norm_rope(x, S, D, 0, H, D, norm_w=w, eps=1e-5))
+    xb = oracle.bf16_to_f32(x)
+    for s in range(S):
+        ss = _shfl_xor_block_sum((xb[s] * xb[s]).astype(np.float32), D)
+        rstd = np.float32(1.0 / np.sqrt(np.float64(np.float32(ss / np.float32(D)) + np.float32(1e-5))))
+        want = oracle.bf16_to_f32(oracle.f32_to_bf16((xb[s] * rstd).astype(np.float32)))
+        assert np.array_equal(out[s, 0], want)
