@@ -228,7 +228,7 @@ __device__ __forceinline__ void pv(const unsigned char* vd, QBlock<DH>& X, const
 // by 8h once, then every test is a compile-time bit position (no per-lane masks).
 // `rel` is the last key of the tile this lane's query may see (causal; >= 63 when
 // every key is visible), so key index kk is kept iff kk <= rel.
-template <int DH>
+template <bool CAUSAL, int DH>
 __device__ __forceinline__ void mask_scores(QBlock<DH>& X, uint64_t live, int rel, const Lane& ln) {
   const uint64_t lv = live >> (ln.h * 8);
   const uint32_t lo = uint32_t(lv), hi = uint32_t(lv >> 32);
@@ -239,7 +239,7 @@ __device__ __forceinline__ void mask_scores(QBlock<DH>& X, uint64_t live, int re
     for (int i = 0; i < 16; ++i) {
       const int bit = kb * 32 + (i >> 3) * 16 + (i & 7);
       const uint32_t w = bit < 32 ? lo : hi;
-      if (!((w >> (bit & 31)) & 1u) || bit > relh) X.s[kb][i] = -__builtin_inff();
+      if (!((w >> (bit & 31)) & 1u) || (CAUSAL && bit > relh)) X.s[kb][i] = -__builtin_inff();
     }
 }
 
@@ -253,9 +253,10 @@ __device__ __forceinline__ int causal_rel(const mx_attn_params& p, int row, int 
 
 // Key tiles one work-group of queries [qbeg, qbeg + QT) needs: all of them, or
 // under the causal mask those up to key q_offset + min(qbeg + QT, Sq) - 1.
+template <bool CAUSAL>
 __device__ __forceinline__ int tiles_needed(const mx_attn_params& p, int qbeg, int QT) {
   const int nt = (p.Skv + KT - 1) / KT;
-  if (!p.causal) return nt;
+  if constexpr (!CAUSAL) return nt;
   const int64_t last = int64_t(p.q_offset) + (qbeg + QT < p.Sq ? qbeg + QT : p.Sq);  // exclusive
   if (last <= 0) return 0;
   const int64_t e = last < p.Skv ? last : p.Skv;
@@ -360,7 +361,7 @@ __device__ __forceinline__ void store_block(const QBlock<DH>& X, uint16_t* o, co
 // lives in stage t % 2 and the loads of tile t + 1 (clamped to the last tile,
 // so the ops are unconditional and interleave with the MFMAs) go into the
 // stage tile t - 1 used.
-template <int DH>
+template <int DH, bool CAUSAL>
 __global__ void __launch_bounds__(512, 1)
 flash_bf16_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
               uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign) {
@@ -377,16 +378,16 @@ flash_bf16_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
   const int ntq = (p.Sq + QT - 1) / QT;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   // causal: query tiles with the most key tiles first
-  const int head = L / ntq, qtile = p.causal ? ntq - 1 - L % ntq : L % ntq;
+  const int head = L / ntq, qtile = CAUSAL ? ntq - 1 - L % ntq : L % ntq;
   const int kvh = head / (p.Hq / p.Hkv);
   const int q0 = qtile * QT + wave * 32;
-  const int nt = tiles_needed(p, qtile * QT, QT);
+  const int nt = tiles_needed<CAUSAL>(p, qtile * QT, QT);
   const int64_t kvbase = int64_t(kvh) * DH;
   const TileAddr ta = tile_addr<NW>(p, wave_u, ln.lane);
 
   QBlock<DH> A;
   qblock_init(A, q, p, q0, head, ln, qsign);
-  if (nt == 0) {  // causal: no visible key for any query of the work-group -> 0
+  if (CAUSAL && nt == 0) {  // causal: no visible key for any query of the work-group -> 0
     store_block(A, o, p, q0, head, ln);
     return;
   }
@@ -405,8 +406,8 @@ flash_bf16_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
     issue(t + 1 < nt ? t + 1 : nt - 1, nxt);
     scores(cur, A, ln);
     sched_k<2 * Dm::NC, OPS>();
-    const bool diag = p.causal && int64_t(p.q_offset) + q0 - int64_t(t) * KT < KT - 1;  // wave-uniform
-    if (live != ~0ull || diag) mask_scores(A, live, diag ? causal_rel(p, q0 + ln.n, t) : KT - 1, ln);
+    const bool diag = CAUSAL && int64_t(p.q_offset) + q0 - int64_t(t) * KT < KT - 1;  // wave-uniform
+    if (live != ~0ull || diag) mask_scores<CAUSAL>(A, live, diag ? causal_rel(p, q0 + ln.n, t) : KT - 1, ln);
     softmax(A, ln);
     rescale(A);
     pv(cur + Dm::KTB, A, ln);
@@ -433,7 +434,7 @@ flash_bf16_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
 // K(t+2) and V(t+1) go into the buffers of K(t) and V(t-1), both last read in
 // period 2t; group A issues all of their DMA ops during its MFMA period 2t+1
 // (8 per wave, one per four MFMAs), and waits for them at the top of tile t+1.
-template <int DH>
+template <int DH, bool CAUSAL>
 __global__ void __launch_bounds__(512, 1)
 flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
               uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign) {
@@ -453,16 +454,16 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
   const int ntq = (p.Sq + QT - 1) / QT;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   // causal: query tiles with the most key tiles first
-  const int head = L / ntq, qtile = p.causal ? ntq - 1 - L % ntq : L % ntq;
+  const int head = L / ntq, qtile = CAUSAL ? ntq - 1 - L % ntq : L % ntq;
   const int kvh = head / (p.Hq / p.Hkv);
   const int q0 = qtile * QT + wave * 32;
-  const int nt = tiles_needed(p, qtile * QT, QT);
+  const int nt = tiles_needed<CAUSAL>(p, qtile * QT, QT);
   const int64_t kvbase = int64_t(kvh) * DH;
   const TileAddr ta8 = tile_addr<8>(p, wave_u, ln.lane);      // prologue: all 8 waves load
   const TileAddr ta4 = tile_addr<4>(p, wave_u & 3, ln.lane);  // loop: group A loads
 
   QBlock<DH> A;
-  if (nt == 0) {  // causal: no visible key for any query of the work-group -> 0
+  if (CAUSAL && nt == 0) {  // causal: no visible key for any query of the work-group -> 0
     qblock_init(A, q, p, q0, head, ln, qsign);
     store_block(A, o, p, q0, head, ln);
     return;
@@ -496,8 +497,8 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
   };
   auto valu_part = [&](int t) __attribute__((always_inline)) {
     const uint64_t live = tile_live<KT>(live_tiles, p, t);
-    const bool diag = p.causal && int64_t(p.q_offset) + q0 - int64_t(t) * KT < KT - 1;  // wave-uniform
-    if (live != ~0ull || diag) mask_scores(A, live, diag ? causal_rel(p, q0 + ln.n, t) : KT - 1, ln);
+    const bool diag = CAUSAL && int64_t(p.q_offset) + q0 - int64_t(t) * KT < KT - 1;  // wave-uniform
+    if (live != ~0ull || diag) mask_scores<CAUSAL>(A, live, diag ? causal_rel(p, q0 + ln.n, t) : KT - 1, ln);
     softmax(A, ln);
     rescale(A);
   };
@@ -553,16 +554,18 @@ hipError_t launch_flash_bf16(const uint16_t* q, const uint16_t* k, const uint16_
   const int64_t blocks = int64_t(ntq) * p.Hq;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
   const dim3 grid{unsigned(blocks)}, block{512};
+  auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, 0, s, q, k, v, o, p, c, qsign); };
+  const bool cz = p.causal != 0;
   switch (p.D) {
     case 128:
 #if MXA_BF16_KIND == 8
-      hipLaunchKernelGGL(flash_bf16_w8<128>, grid, block, 0, s, q, k, v, o, p, c, qsign);
+      cz ? go(flash_bf16_w8<128, true>) : go(flash_bf16_w8<128, false>);
 #else
-      hipLaunchKernelGGL(flash_bf16_pp<128>, grid, block, 0, s, q, k, v, o, p, c, qsign);
+      cz ? go(flash_bf16_pp<128, true>) : go(flash_bf16_pp<128, false>);
 #endif
       break;
-    case 64: hipLaunchKernelGGL(flash_bf16_pp<64>, grid, block, 0, s, q, k, v, o, p, c, qsign); break;
-    case 72: hipLaunchKernelGGL(flash_bf16_pp<72>, grid, block, 0, s, q, k, v, o, p, c, qsign); break;
+    case 64: cz ? go(flash_bf16_pp<64, true>) : go(flash_bf16_pp<64, false>); break;
+    case 72: cz ? go(flash_bf16_pp<72, true>) : go(flash_bf16_pp<72, false>); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
