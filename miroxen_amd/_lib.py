@@ -35,7 +35,8 @@ class CParams(ctypes.Structure):
 
 class CLayout(ctypes.Structure):
     _fields_ = [("sq_pad", ctypes.c_int64), ("skv_pad", ctypes.c_int64)] + [
-        (n, ctypes.c_size_t) for n in ("qi", "ki", "vt", "qs", "ks", "km", "va", "part", "total")]
+        (n, ctypes.c_size_t) for n in ("qi", "ki", "vt", "qs", "ks", "km", "va", "part", "split", "cnt", "total")] + [
+        ("split_units", ctypes.c_int), ("split_parts", ctypes.c_int)]
 
 
 _lib = None

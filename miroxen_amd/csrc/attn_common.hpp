@@ -14,6 +14,7 @@ using bf16x8 = __attribute__((ext_vector_type(8))) __bf16;
 using bf16x4 = __attribute__((ext_vector_type(4))) __bf16;
 using f32x16 = __attribute__((ext_vector_type(16))) float;
 using f32x4 = __attribute__((ext_vector_type(4))) float;
+using f32x2 = __attribute__((ext_vector_type(2))) float;
 using i32x16 = __attribute__((ext_vector_type(16))) int;
 using i32x8 = __attribute__((ext_vector_type(8))) int;
 using i32x4 = __attribute__((ext_vector_type(4))) int;
@@ -34,7 +35,6 @@ __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(uint3
 __device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  using f32x2 = __attribute__((ext_vector_type(2))) float;
   using bf16x2 = __attribute__((ext_vector_type(2))) __bf16;
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
 }

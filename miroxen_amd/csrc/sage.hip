@@ -15,13 +15,6 @@
 
 namespace mxa {
 
-#ifdef MXA_PPT
-__device__ uint64_t* g_ppt = nullptr;
-extern "C" int mx_debug_ppt(void* buf) {
-  return hipMemcpyToSymbol(HIP_SYMBOL(g_ppt), &buf, sizeof(buf)) == hipSuccess ? 0 : -2;
-}
-#endif
-
 namespace {
 
 constexpr int D = 128;
@@ -123,8 +116,11 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
 
 // kmean = sum of the partials in ascending block order from 0.f; vamax = max.
 __global__ void __launch_bounds__(D) prep_finalize(mx_attn_params p, int nb, const float* __restrict__ part,
-                                                   float* __restrict__ km, float* __restrict__ va) {
+                                                   float* __restrict__ km, float* __restrict__ va,
+                                                   int* __restrict__ cnt, int ncnt) {
   const int h = blockIdx.x, d = threadIdx.x;
+  if (h == 0)  // arrival counters of the attention kernel's split units start at zero
+    for (int i = d; i < ncnt; i += D) cnt[i] = 0;
   const float* ps = part + int64_t(h) * nb * D + d;
   const float* pa = ps + int64_t(p.Hkv) * nb * D;
   float s = 0.f, am = 0.f;
@@ -251,16 +247,26 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
 // Tiles arrive by buffer_load ... lds (no VGPR staging), one K and one V^T op per
 // wave per tile, placed between the score MFMAs of the previous tile.
 //
-// Two work-group schedules (MXA_SAGE_KIND): 8 (default) lockstep, every wave
-// runs S -> softmax -> P*V per tile; 9 ping-pong, as the BF16 kernel's default.
-// The softmax here is the larger share of the work (the INT8/FP8 MFMAs take half
-// the cycles of BF16 ones), and a single wave alone on a SIMD runs it slower than
-// two interleaved waves, so lockstep measures ~10% faster.
+// Schedule: lockstep, every wave runs S -> softmax -> P*V per tile. The softmax
+// is the larger share of the work here (the INT8/FP8 MFMAs take half the cycles
+// of BF16 ones) and bounds the kernel. A ping-pong schedule like the BF16
+// kernel's was measured ~10% slower: a wave running the softmax alone on a SIMD
+// does not get the dual issue of fp32 adds/FMAs that two interleaved waves get,
+// and a neighbouring MFMA wave slows it by a further 20-30%.
 
 constexpr int KT = 64;
 constexpr int KTILEB = KT * D;        // 8 KB int8 K tile
 constexpr int VTILEB = D * KT;        // 8 KB fp8 V^T tile
 constexpr int STAGEB = KTILEB + VTILEB;
+// Split partial of one work-group (see sage_plan): acc as [8 waves][16 float4]
+// [64 lanes], then m and l as [8 waves][64 lanes][2].
+constexpr int kSplitAcc = 8 * 16 * 64 * 4, kSplitFloats = kSplitAcc + 8 * 64 * 2;
+constexpr int kMaxParts = 4;  // bounds the merge's reads (parts x 132 KB per unit)
+struct SageSplit {
+  int full, parts;  // work-groups [0, full) run whole units; the rest run one of `parts` key ranges
+  float* part;      // partials, kSplitFloats per split work-group
+  int* cnt;         // arrival counter per split unit
+};
 constexpr float kSageHeadroom = 2.f;
 constexpr int kScoreBias = 0x4B400000;  // bits of 12582912.0f = 1.5 * 2^23
 constexpr i32x16 kScoreBias16 = {kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
@@ -269,9 +275,63 @@ constexpr i32x16 kScoreBias16 = {kScoreBias, kScoreBias, kScoreBias, kScoreBias,
 #ifndef MXA_SAGE_NS
 #define MXA_SAGE_NS 2
 #endif
-#ifndef MXA_SAGE_KIND
-#define MXA_SAGE_KIND 8
-#endif
+
+// Online-softmax step of one lane over the 32 biased int32 scores of a tile
+// (reference attention_fp8.cu:306-345): integer row max, sc = qs * ks, one FMA into
+// exp2, P packed to e4m3 four at a time (byte j of the 32-byte B operand is key
+// 32h + j, j = kb*16 + ii), l over the unquantized values. Dead keys (mask, tail)
+// get the bits of -inf: below every biased score as an integer (so the integer max
+// skips them) and, as a float, exp2(fma(-inf, sc, nm)) = 0 exactly for sc > 0 (sc is
+// clamped to >= 1e-30, which moves no live exponent). The max and the sum are
+// trees and the 32 exponentials are independent, so a wave running this alone
+// (ping-pong) is bound by VALU throughput rather than by dependency latency.
+// Returns alpha, the rescale factor of the running output.
+constexpr int kDead = int(0xFF800000u);
+__device__ __forceinline__ float sage_softmax(i32x16 (&s)[2], uint64_t live, int h, float sc, float& m, float& l,
+                                              i32x8& pf) {
+  if (live != ~0ull) {
+    // this lane's 32 keys are bits 32h .. 32h+31: select the word once, then every
+    // test is a compile-time bit position (no per-lane mask registers)
+    const uint32_t lw = h ? uint32_t(live >> 32) : uint32_t(live);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int ii = 0; ii < 16; ++ii)
+        if (!((lw >> (kb * 16 + ii)) & 1u)) s[kb][ii] = kDead;
+  }
+  auto S = [&](int i) __attribute__((always_inline)) { return s[i >> 4][i & 15]; };
+  int a[11];
+#pragma unroll
+  for (int i = 0; i < 10; ++i) a[i] = max(max(S(3 * i), S(3 * i + 1)), S(3 * i + 2));
+  a[10] = max(S(30), S(31));
+  const int b0 = max(max(a[0], a[1]), a[2]), b1 = max(max(a[3], a[4]), a[5]);
+  const int b2 = max(max(a[6], a[7]), a[8]), b3 = max(a[9], a[10]);
+  int im = max(max(b0, b1), max(b2, b3));
+  im = max(im, other_half_i(im));
+  const float tmax = im == kDead ? -__builtin_inff() : float(im - kScoreBias) * sc;
+  const float mnew = tmax > m + kSageHeadroom ? tmax : m;
+  const float alpha = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+  m = mnew;
+  // exponent = (12582912 + s)*sc + nm with nm = (log2 448 - H - m) - 12582912*sc
+  // (reference attention_fp8.cu:331, :337, plus the headroom H)
+  const float nm =
+      mnew == -__builtin_inff() ? -__builtin_inff() : (kLog2_448 - kSageHeadroom - mnew) - 12582912.f * sc;
+  float e[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(__int_as_float(S(i)), sc, nm));
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    const uint32_t lo = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(e[4 * w], e[4 * w + 1], 0, false));
+    pf[w] = __builtin_amdgcn_cvt_pk_fp8_f32(e[4 * w + 2], e[4 * w + 3], int(lo), true);
+  }
+#pragma unroll
+  for (int w = 16; w >= 1; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w; ++i) e[i] += e[i + w];
+  const float ts = e[0] + other_half(e[0]);
+  l = l * alpha + ts;
+  return alpha;
+}
 
 // Score row m of key block kb -> key within the 64-key tile.
 __device__ __forceinline__ int kperm(int kb, int m) {
@@ -321,7 +381,7 @@ template <int NS>
 __global__ void __launch_bounds__(512, 1)
 sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, const uint8_t* __restrict__ vt,
                const float* __restrict__ qs, const float* __restrict__ ks, const float* __restrict__ va,
-               uint16_t* __restrict__ o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad) {
+               uint16_t* __restrict__ o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad, SageSplit sp) {
   constexpr int NW = 8, QT = NW * 32, OPS = 2 * (8 / NW);
   static_assert(NS >= 2 && NS <= 4, "2..4 stages");
   __shared__ __align__(16) unsigned char st0[STAGEB];
@@ -338,20 +398,34 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   };
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 31, h = lane >> 5;
   const int ntq = (p.Sq + QT - 1) / QT;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int nkt = (p.Skv + KT - 1) / KT;
+  // unit (head, query tile) and key-tile range [tb, nt) of this work-group
+  int L, tb = 0, nt = nkt, su = 0, part = -1;
+  if (int(blockIdx.x) < sp.full) {
+    L = xcd_remap(blockIdx.x, sp.full);
+  } else {
+    // part-major order (part 0 of every split unit, then part 1, ...): the last
+    // arrivals, which also merge, fall in the grid's last batch instead of delaying
+    // the dispatch of the batches before it
+    const int j = int(blockIdx.x) - sp.full, nsu = (int(gridDim.x) - sp.full) / sp.parts;
+    part = j / nsu;
+    su = j - part * nsu;
+    L = sp.full + su;
+    tb = int(int64_t(part) * nkt / sp.parts);
+    nt = int(int64_t(part + 1) * nkt / sp.parts);
+  }
   const int head = L / ntq, qtile = L % ntq;
   const int kvh = head / (p.Hq / p.Hkv);
   const int q0 = qtile * QT + wave * 32;
-  const int nt = (p.Skv + KT - 1) / KT;
 
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const SageAddr sa = sage_addr(ki, vt, kvh, skv_pad, wave_u, lane);
   auto issue = [&](int t, unsigned char* dst) __attribute__((always_inline)) {
     sage_load_tile<NW>(sa, t, t, dst, dst + KTILEB, wave_u, skv_pad);
   };
-  issue(0, stage(std::integral_constant<int, 0>{}));
-  if constexpr (NS > 2) if (1 < nt) issue(1, stage(std::integral_constant<int, 1>{}));
-  if constexpr (NS > 3) if (2 < nt) issue(2, stage(std::integral_constant<int, 2>{}));
+  issue(tb, stage(std::integral_constant<int, 0>{}));
+  if constexpr (NS > 2) if (tb + 1 < nt) issue(tb + 1, stage(std::integral_constant<int, 1>{}));
+  if constexpr (NS > 3) if (tb + 2 < nt) issue(tb + 2, stage(std::integral_constant<int, 2>{}));
 
   // Q^T fragments: lane (n, h) holds 16 int8 channels 32c + 16h .. +15 of its query.
   const int row = q0 + n;  // < sq_pad (sq_pad is a multiple of QT)
@@ -363,7 +437,7 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   }
   const float qscale = qs[int64_t(head) * (sq_pad / 16) + row / 16];
   const float* kscale = ks + int64_t(kvh) * (skv_pad / KT);
-  build_live<NW, KT>(live_tiles, p, nt, wave, lane);
+  build_live<NW, KT>(live_tiles, p, nkt, wave, lane);
   __syncthreads();  // bitmaps visible (once, before the pipelined loop)
 
   // Per-lane LDS read bases.
@@ -377,10 +451,6 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
 #pragma unroll
   for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
   float m = -__builtin_inff(), l = 0.f;
-  // Dead keys get the bits of -inf: below every biased score as an integer (so the
-  // integer max skips them) and, as a float, exp2(fma(-inf, sc, nm)) = 0 exactly
-  // for sc > 0 (sc is clamped to >= 1e-30, which moves no live exponent).
-  constexpr int kDead = int(0xFF800000u);
 
   auto step = [&](int t, auto i) __attribute__((always_inline)) {
     const unsigned char* sd = stage(i);
@@ -411,54 +481,8 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
       if (j < 5) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
 
-    if (live != ~0ull) {
-      // this lane's 32 keys are bits 32h .. 32h+31: select the word once, then
-      // every test is a compile-time bit position (no per-lane mask registers)
-      const uint32_t lw = h ? uint32_t(live >> 32) : uint32_t(live);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int ii = 0; ii < 16; ++ii)
-          if (!((lw >> (kb * 16 + ii)) & 1u)) s[kb][ii] = kDead;
-    }
-    int im = s[0][0];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int ii = 0; ii < 16; ++ii) im = max(im, s[kb][ii]);
-    im = max(im, other_half_i(im));
-    const float sc = fmaxf(qscale * ksc, 1e-30f);
-    const float tmax = im == kDead ? -__builtin_inff() : float(im - kScoreBias) * sc;
-    const float mnew = tmax > m + kSageHeadroom ? tmax : m;
-    const float alpha = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
-    m = mnew;
-    // exponent = (12582912 + s)*sc + nm with nm = (log2 448 - H - m) - 12582912*sc
-    // (reference attention_fp8.cu:331, :337, plus the headroom H)
-    const float nm =
-        mnew == -__builtin_inff() ? -__builtin_inff() : (kLog2_448 - kSageHeadroom - mnew) - 12582912.f * sc;
-    // P = 2^exponent packed to e4m3 four at a time: byte j of the 32-byte B operand
-    // is key 32h + j (j = kb*16 + ii); l sums the unquantized values
-    float ts = 0.f;
     i32x8 pf;
-    auto pexp = [&](int si, auto masked) __attribute__((always_inline)) -> float {
-      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(__int_as_float(si), sc, nm));
-      if constexpr (decltype(masked)::value) return si == kDead ? 0.f : e;
-      return e;
-    };
-    auto pack = [&](auto masked) __attribute__((always_inline)) {
-#pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        const int kb = w >> 2, i0 = (w & 3) * 4;
-        const float e0 = pexp(s[kb][i0], masked), e1 = pexp(s[kb][i0 + 1], masked);
-        const float e2 = pexp(s[kb][i0 + 2], masked), e3 = pexp(s[kb][i0 + 3], masked);
-        ts += (e0 + e1) + (e2 + e3);
-        const uint32_t lo = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(e0, e1, 0, false));
-        pf[w] = __builtin_amdgcn_cvt_pk_fp8_f32(e2, e3, int(lo), true);
-      }
-    };
-    pack(std::false_type{});
-    ts += other_half(ts);
-    l = l * alpha + ts;
+    const float alpha = sage_softmax(s, live, h, fmaxf(qscale * ksc, 1e-30f), m, l, pf);
     if (!__all(alpha == 1.f)) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) acc[db] *= alpha;
@@ -479,7 +503,7 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
       if (j < 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
   };
-  for (int t = 0; t < nt; t += NS) {
+  for (int t = tb; t < nt; t += NS) {
     step(t, std::integral_constant<int, 0>{});
     if (t + 1 < nt) step(t + 1, std::integral_constant<int, 1>{});
     if constexpr (NS > 2) if (t + 2 < nt) step(t + 2, std::integral_constant<int, 2>{});
@@ -487,221 +511,68 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   }
 
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
-  // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----
-  if (row < p.Sq) {
-    const float* vah = va + kvh * D;
-    const float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
-    uint16_t* dst = o + int64_t(row) * p.o_stride + head * D + h * 4;
+  if (part >= 0) {
+    // Split unit: publish (acc, m, l), then the last part to arrive merges all parts.
+    // The partials move with device-scope (sc1) buffer accesses, which bypass the
+    // XCDs' non-coherent L2s for these lines only; a device-scope fence would write
+    // back and invalidate a whole L2 and with it every other work-group's K/V.
+    constexpr int kSc1 = 16;  // cache policy: device scope
+    const uint32_t unit_bytes = uint32_t(sp.parts) * kSplitFloats * 4;
+    const __amdgpu_buffer_rsrc_t rp = buf_rsrc(sp.part + int64_t(su) * sp.parts * kSplitFloats, unit_bytes);
+    const uint32_t lacc = uint32_t(wave * 16 * 64 + lane) * 16u;          // + j * 1024 for float4 j
+    const uint32_t lml = uint32_t(kSplitAcc + (wave * 64 + lane) * 2) * 4u;
+    const uint32_t mine = uint32_t(part) * kSplitFloats * 4u;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = db * 32 + g * 8 + h * 4;
-        const f32x4 sv = *reinterpret_cast<const f32x4*>(vah + d);
-        uint32_t* d32 = reinterpret_cast<uint32_t*>(dst + db * 32 + g * 8);
-        d32[0] = pack_bf16x2(acc[db][g * 4] * sv[0] * inv, acc[db][g * 4 + 1] * sv[1] * inv);
-        d32[1] = pack_bf16x2(acc[db][g * 4 + 2] * sv[2] * inv, acc[db][g * 4 + 3] * sv[3] * inv);
-      }
+      for (int g = 0; g < 4; ++g)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, f32x4{acc[db][g * 4], acc[db][g * 4 + 1], acc[db][g * 4 + 2], acc[db][g * 4 + 3]}),
+            rp, lacc + uint32_t(db * 4 + g) * 1024u, mine, kSc1);
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m, l}), rp, lml, mine, kSc1);
+    wait_vm();  // this lane's partial has reached the device-coherent level
+    __shared__ int last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int prev = __hip_atomic_fetch_add(sp.cnt + su, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = prev == sp.parts - 1;
+      if (last) __hip_atomic_store(sp.cnt + su, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+    }
+    __syncthreads();
+    if (!last) return;
+    // merge in part order (every part read back, this one's included, so the result
+    // does not depend on which part arrived last): M = max m_i, w_i = 2^(m_i - M),
+    // l = sum l_i w_i, acc = sum acc_i w_i
+    float mi[8], li[8];
+    float mm = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i >= sp.parts) break;
+      const f32x2 ml = __builtin_bit_cast(
+          f32x2, __builtin_amdgcn_raw_buffer_load_b64(rp, lml, uint32_t(i) * kSplitFloats * 4u, kSc1));
+      mi[i] = ml[0];
+      li[i] = ml[1];
+      mm = fmaxf(mm, ml[0]);
+    }
+    l = 0.f;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i >= sp.parts) break;
+      const float wi = mm == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(mi[i] - mm);
+      l += li[i] * wi;
+      f32x4 x[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        x[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rp, lacc + uint32_t(j) * 1024u, uint32_t(i) * kSplitFloats * 4u, kSc1));
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[j >> 2][(j & 3) * 4 + e] += x[j][e] * wi;
+    }
   }
-}
-
-// ---------------- ping-pong variant ----------------
-// Same data flow, but waves w and w + 4 (one SIMD) run the per-tile program one
-// period apart: in each period one issues the MFMAs (P V(t), S(t+1)) while the
-// other runs the softmax, separated by two work-group barriers per tile:
-//   period 2t+1: A: P V(t), S(t+1)    B: softmax(t)
-//   period 2t+2: A: softmax(t+1)       B: P V(t), S(t+1)
-// Group A issues the DMA of K(t+2) and V(t+1) (into the buffers of K(t) and
-// V(t-1), last read in period 2t) between its MFMAs in period 2t+1.
-__global__ void __launch_bounds__(512, 1)
-sage_attn_d128_pp(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, const uint8_t* __restrict__ vt,
-                  const float* __restrict__ qs, const float* __restrict__ ks, const float* __restrict__ va,
-                  uint16_t* __restrict__ o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad) {
-  constexpr int NW = 8, QT = NW * 32;
-  __shared__ __align__(16) unsigned char kb0[KTILEB];
-  __shared__ __align__(16) unsigned char kb1[KTILEB];
-  __shared__ __align__(16) unsigned char vb0[VTILEB];
-  __shared__ __align__(16) unsigned char vb1[VTILEB];
-  __shared__ uint64_t live_tiles[kMaxLiveTiles];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 31, h = lane >> 5;
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const bool group_a = wave < 4;
-  const int ntq = (p.Sq + QT - 1) / QT;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int head = L / ntq, qtile = L % ntq;
-  const int kvh = head / (p.Hq / p.Hkv);
-  const int q0 = qtile * QT + wave * 32;
-  const int nt = (p.Skv + KT - 1) / KT;
-  const SageAddr sa8 = sage_addr(ki, vt, kvh, skv_pad, wave_u, lane);
-  const SageAddr sa4 = sage_addr(ki, vt, kvh, skv_pad, wave_u & 3, lane);
-  sage_load_tile<8>(sa8, 0, 0, kb0, vb0, wave_u, skv_pad);
-  if (nt > 1) sage_load_k<8>(sa8, 1, kb1, wave_u);
-
-  const int row = q0 + n;  // < sq_pad (sq_pad is a multiple of QT)
-  i32x4 qf[4];
-  {
-    const int8_t* src = qi + (int64_t(head) * sq_pad + row) * D + h * 16;
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) qf[cc] = *reinterpret_cast<const i32x4*>(src + cc * 32);
-  }
-  const float qscale = qs[int64_t(head) * (sq_pad / 16) + row / 16];
-  const float* kscale = ks + int64_t(kvh) * (skv_pad / KT);
-  build_live<NW, KT>(live_tiles, p, nt, wave, lane);
-
-  const int krow = kperm(0, n);
-  const int kbase = krow * 32 + ((h ^ ((krow >> 5) & 1)) << 4);
-  const int vsw = (n >> 2) & 3;
-  const int vbase0 = n * 64 + (((2 * h) ^ vsw) << 4);
-  const int vbase1 = n * 64 + (((2 * h + 1) ^ vsw) << 4);
-
-  f32x16 acc[4];
-#pragma unroll
-  for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
-  float m = -__builtin_inff(), l = 0.f;
-  // Dead keys get the bits of -inf: below every biased score as an integer (so the
-  // integer max skips them) and, as a float, exp2(fma(-inf, sc, nm)) = 0 exactly
-  // for sc > 0 (sc is clamped to >= 1e-30, which moves no live exponent).
-  constexpr int kDead = int(0xFF800000u);
-  i32x16 s[2];  // biased int32 scores of the pending tile
-  i32x8 pf;     // P of the pending tile (e4m3)
-
-  auto scores = [&](const unsigned char* kd, auto ld) __attribute__((always_inline)) {
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const i32x4 a = *reinterpret_cast<const i32x4*>(kd + kbase + cc * 2048 + kb * 512);
-        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[cc], cc == 0 ? kScoreBias16 : s[kb], 0, 0, 0);
-      }
-    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (decltype(ld)::value && (j == 1 || j == 5)) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      if (j < 5) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-  };
-  auto pv = [&](const unsigned char* vd, auto ld) __attribute__((always_inline)) {
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const i32x4 a0 = *reinterpret_cast<const i32x4*>(vd + vbase0 + db * 2048);
-      const i32x4 a1 = *reinterpret_cast<const i32x4*>(vd + vbase1 + db * 2048);
-      const i32x8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, pf, acc[db], 0, 0, 0, 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (decltype(ld)::value) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      if (j < 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-  };
-  auto softmax = [&](int t) __attribute__((always_inline)) {
-    const uint64_t live = tile_live<KT>(live_tiles, p, t);
-    if (live != ~0ull) {
-      // this lane's 32 keys are bits 32h .. 32h+31: select the word once, then
-      // every test is a compile-time bit position (no per-lane mask registers)
-      const uint32_t lw = h ? uint32_t(live >> 32) : uint32_t(live);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int ii = 0; ii < 16; ++ii)
-          if (!((lw >> (kb * 16 + ii)) & 1u)) s[kb][ii] = kDead;
-    }
-    int im = s[0][0];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int ii = 0; ii < 16; ++ii) im = max(im, s[kb][ii]);
-    im = max(im, other_half_i(im));
-    const float sc = fmaxf(qscale * kscale[t], 1e-30f);
-    const float tmax = im == kDead ? -__builtin_inff() : float(im - kScoreBias) * sc;
-    const float mnew = tmax > m + kSageHeadroom ? tmax : m;
-    const float alpha = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
-    m = mnew;
-    const float nm =
-        mnew == -__builtin_inff() ? -__builtin_inff() : (kLog2_448 - kSageHeadroom - mnew) - 12582912.f * sc;
-    float ts = 0.f;
-    auto pexp = [&](int si, auto masked) __attribute__((always_inline)) -> float {
-      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(__int_as_float(si), sc, nm));
-      if constexpr (decltype(masked)::value) return si == kDead ? 0.f : e;
-      return e;
-    };
-    auto pack = [&](auto masked) __attribute__((always_inline)) {
-#pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        const int kb = w >> 2, i0 = (w & 3) * 4;
-        const float e0 = pexp(s[kb][i0], masked), e1 = pexp(s[kb][i0 + 1], masked);
-        const float e2 = pexp(s[kb][i0 + 2], masked), e3 = pexp(s[kb][i0 + 3], masked);
-        ts += (e0 + e1) + (e2 + e3);
-        const uint32_t lo = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(e0, e1, 0, false));
-        pf[w] = __builtin_amdgcn_cvt_pk_fp8_f32(e2, e3, int(lo), true);
-      }
-    };
-    pack(std::false_type{});
-    ts += other_half(ts);
-    l = l * alpha + ts;
-    if (!__all(alpha == 1.f)) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-    }
-  };
-  // MFMA period of tile t (S(t+1) on a stale buffer when t + 1 == nt is never read).
-  auto mfma_part = [&](int t, const unsigned char* kc1, const unsigned char* vcur, unsigned char* kfree,
-                       unsigned char* vfree, auto ld) __attribute__((always_inline)) {
-    __builtin_amdgcn_s_setprio(1);
-    if constexpr (decltype(ld)::value)  // K(t+2), V(t+1), clamped so the ops are unconditional
-      sage_load_tile<4>(sa4, t + 2 < nt ? t + 2 : nt - 1, t + 1 < nt ? t + 1 : nt - 1, kfree, vfree, wave_u & 3,
-                        skv_pad);
-    pv(vcur, ld);
-    scores(kc1, ld);
-    __builtin_amdgcn_s_setprio(0);
-  };
-
-  wait_vm_n<0>();
-  __syncthreads();  // K(0), V(0), K(1) and the liveness bitmaps are visible
-  if (group_a) scores(kb0, std::false_type{});  // period -1: S_A(0)
-  block_sync();
-  if (group_a) softmax(0);  // period 0: A softmax(0), B S_B(0)
-  else scores(kb0, std::false_type{});
-
-  // Tile t: kc1 = K(t+1), vcur = V(t); kfree / vfree receive K(t+2) / V(t+1).
-#ifdef MXA_PPT
-  uint64_t pt0 = 0, pt1 = 0, pt2 = 0, pt3 = 0, pt4 = 0;
-#define MXA_PT(v) do { if (t == 20) { __builtin_amdgcn_sched_barrier(0); v = __builtin_amdgcn_s_memtime(); __builtin_amdgcn_sched_barrier(0); } } while (0)
-#else
-#define MXA_PT(v) do { } while (0)
-#endif
-  auto tile = [&](int t, const unsigned char* kc1, const unsigned char* vcur, unsigned char* kfree,
-                  unsigned char* vfree) __attribute__((always_inline)) {
-    MXA_PT(pt0);
-    wait_vm_n<0>();  // group A: its DMA of K(t+1), V(t) landed
-    block_sync();
-    MXA_PT(pt1);
-    if (group_a) mfma_part(t, kc1, vcur, kfree, vfree, std::true_type{});
-    else softmax(t);
-    MXA_PT(pt2);
-    block_sync();
-    MXA_PT(pt3);
-    if (group_a) {
-      if (t + 1 < nt) softmax(t + 1);
-    } else {
-      mfma_part(t, kc1, vcur, kfree, vfree, std::false_type{});
-    }
-    MXA_PT(pt4);
-  };
-  for (int t = 0; t < nt; t += 2) {
-    tile(t, kb1, vb0, kb0, vb1);
-    if (t + 1 < nt) tile(t + 1, kb0, vb1, kb1, vb0);
-  }
-  wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
-#ifdef MXA_PPT
-  if (lane == 0 && g_ppt) {
-    uint64_t* d = g_ppt + (int64_t(blockIdx.x) * 8 + wave) * 5;
-    d[0] = pt0; d[1] = pt1; d[2] = pt2; d[3] = pt3; d[4] = pt4;
-  }
-#endif
   // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----
   if (row < p.Sq) {
     const float* vah = va + kvh * D;
@@ -723,8 +594,52 @@ sage_attn_d128_pp(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, 
 }  // namespace
 
 // Workspace carve-up (kept in one place for the host code and the kernels).
+// Work split of the attention grid. One work-group (8 waves, 256 queries of one
+// head) fills a CU, so a grid of U units on C CUs runs in ceil(U / C) rounds and
+// the last one leaves CUs idle when C does not divide U (config 2: 408 units on 256
+// CUs, 1.59 rounds of work in 2). The last U % C units are therefore split by key
+// range into S parts, S chosen to minimise the tail's length ceil(r S / C) / S in
+// units (config 2: S = 3, tail 2/3 of a unit instead of 1); each part writes its
+// unnormalised output and the last part to finish merges them.
+struct SagePlan {
+  int full;   // work-groups that run a whole unit (a multiple of C, or all units)
+  int units;  // split units (the last `units` units of the grid)
+  int parts;  // parts per split unit
+};
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+SagePlan sage_plan(const mx_attn_params& p) {
+  constexpr int QT = 256;
+  const int64_t ntq = (int64_t(p.Sq) + QT - 1) / QT, U64 = ntq * p.Hq;
+  const int nt = (p.Skv + kKvPad - 1) / kKvPad;
+  const int C = device_cus();
+  SagePlan pl{int(U64 < 0x7fffffff ? U64 : 0x7fffffff), 0, 1};
+  if (C <= 0 || U64 >= 0x7fffffff) return pl;
+  const int U = int(U64), r = U % C;
+  if (r == 0) return pl;
+  double best = 1.0;
+  for (int S = 2; S <= kMaxParts && S * 4 <= nt; ++S) {  // parts of >= 4 key tiles
+    const double cost = double((int64_t(r) * S + C - 1) / C) / S;
+    if (cost < best - 1e-9) best = cost, pl.parts = S;
+  }
+  if (pl.parts > 1) pl.full = U - r, pl.units = r;
+  return pl;
+}
+
 mx_sage_layout sage_layout(const mx_attn_params& p) {
   mx_sage_layout L{};
+  const SagePlan pl = sage_plan(p);
+  L.split_units = pl.units;
+  L.split_parts = pl.parts;
   L.sq_pad = (int64_t(p.Sq) + kSqPad - 1) / kSqPad * kSqPad;
   L.skv_pad = (int64_t(p.Skv) + kKvPad - 1) / kKvPad * kKvPad;
   const int64_t nb = (int64_t(p.Skv) + kStatTok - 1) / kStatTok;
@@ -742,6 +657,8 @@ mx_sage_layout sage_layout(const mx_attn_params& p) {
   L.km = take(sizeof(float) * p.Hkv * p.D);
   L.va = take(sizeof(float) * p.Hkv * p.D);
   L.part = take(sizeof(float) * 2 * p.Hkv * nb * p.D);
+  L.split = take(sizeof(float) * kSplitFloats * size_t(pl.units) * pl.parts);
+  L.cnt = take(sizeof(int) * size_t(pl.units));
   L.total = off;
   return L;
 }
@@ -761,7 +678,8 @@ hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint
   const float qmult = p.scale * kLog2e;
   hipLaunchKernelGGL(prep_stats_q, dim3(unsigned(blocks1)), dim3(256), 0, s, q, k, v, p, nb, qmult, L.sq_pad, part,
                      reinterpret_cast<int8_t*>(ws + L.qi), reinterpret_cast<float*>(ws + L.qs));
-  hipLaunchKernelGGL(prep_finalize, dim3(p.Hkv), dim3(D), 0, s, p, nb, (const float*)part, km, va);
+  hipLaunchKernelGGL(prep_finalize, dim3(p.Hkv), dim3(D), 0, s, p, nb, (const float*)part, km, va,
+                     reinterpret_cast<int*>(ws + L.cnt), L.split_units);
   hipLaunchKernelGGL(prep_kv_quant, dim3(unsigned(L.skv_pad / kKvPad), p.Hkv), dim3(256), 0, s, k, v, p, L.skv_pad,
                      (const float*)km, (const float*)va, reinterpret_cast<int8_t*>(ws + L.ki),
                      reinterpret_cast<float*>(ws + L.ks), reinterpret_cast<uint8_t*>(ws + L.vt));
@@ -773,17 +691,17 @@ hipError_t launch_sage_attend(uint16_t* o, const mx_attn_params& p, const char* 
   static_assert(kSqPad % QT == 0, "Q padding must cover whole query tiles");
   const mx_sage_layout L = sage_layout(p);
   const int ntq = (p.Sq + QT - 1) / QT;
-  const int64_t blocks = int64_t(ntq) * p.Hq;
-  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-#if MXA_SAGE_KIND == 9
-  hipLaunchKernelGGL(sage_attn_d128_pp, dim3(unsigned(blocks)), dim3(512), 0, s,
-#else
+  const int64_t units = int64_t(ntq) * p.Hq;
+  if (units > 0x7fffffff) return hipErrorInvalidValue;
+  const SageSplit sp{int(units) - L.split_units, L.split_parts,
+                     reinterpret_cast<float*>(const_cast<char*>(ws) + L.split),
+                     reinterpret_cast<int*>(const_cast<char*>(ws) + L.cnt)};
+  const int64_t blocks = int64_t(sp.full) + int64_t(L.split_units) * L.split_parts;
   hipLaunchKernelGGL((sage_attn_d128<MXA_SAGE_NS>), dim3(unsigned(blocks)), dim3(512), 0, s,
-#endif
                      reinterpret_cast<const int8_t*>(ws + L.qi), reinterpret_cast<const int8_t*>(ws + L.ki),
                      reinterpret_cast<const uint8_t*>(ws + L.vt), reinterpret_cast<const float*>(ws + L.qs),
                      reinterpret_cast<const float*>(ws + L.ks), reinterpret_cast<const float*>(ws + L.va), o, p,
-                     L.sq_pad, L.skv_pad);
+                     L.sq_pad, L.skv_pad, sp);
   return hipGetLastError();
 }
 

@@ -251,13 +251,73 @@ void or_v_quant(const uint16_t* v, int Skv, int Hkv, int D, int64_t kv_stride, i
  * bit-trick formulation operation for operation (:331, :337).
  * exp2 here is libm's double exp2 rounded to float (the GPU uses v_exp_f32,
  * < 1 ulp). out: [n_rows][Hq][D] f32 (before the bf16 store). */
+/* One key-tile range [t0, t1) of one (row, head): updates m, l, acc in place. */
+static void or_sage_range(const int8_t* qr, float qscale, const int8_t* ki, const uint8_t* vt, const float* ksh,
+                          int kvh, int Skv, int D, int64_t skv_pad, const uint8_t* kv_valid, const float* lut,
+                          float headroom, int t0, int t1, float* m_io, float* l_io, float* acc) {
+  const float L448 = 8.807354922057604f;
+  float m = *m_io, l = *l_io;
+  int32_t s[64];
+  float f[64];
+  for (int t = t0; t < t1; ++t) {
+    const float sc = qscale * ksh[t];
+    int live_any = 0;
+    int32_t im = INT32_MIN;
+    for (int j = 0; j < 64; ++j) {
+      int64_t key = (int64_t)t * 64 + j;
+      int live = key < Skv && (!kv_valid || kv_valid[key]);
+      const int8_t* kr = ki + ((int64_t)kvh * skv_pad + key) * D;
+      int32_t dot = 0;
+      for (int d = 0; d < D; ++d) dot += (int32_t)qr[d] * (int32_t)kr[d];
+      s[j] = live ? dot : INT32_MIN;
+      if (live) { live_any = 1; if (dot > im) im = dot; }
+    }
+    if (!live_any) continue;
+    const float tmax = (float)im * sc;
+    /* headroom 0: next = max(m, tmax), the reference rule (:327). headroom H > 0:
+     * lazy max, m moves only when the tile max exceeds it by more than H, and P
+     * carries 2^-H so it stays <= 448 (this build's kernel uses H = 2). */
+    float next = tmax > m + headroom ? tmax : m;
+    float alpha = m == -INFINITY ? 0.f : (float)exp2((double)(m - next));
+    m = next;
+    /* exponent as the reference computes it (:331, :337): the int32 score is read as
+     * the float 12582912 + s through its bits (s + 0x4B400000), one FMA with
+     * nm = (log2 448 - H - next) - 12582912*sc (two float roundings). */
+    const float nm = (L448 - headroom - next) - 12582912.f * sc;
+    float ts = 0.f;
+    for (int j = 0; j < 64; ++j) {
+      if (s[j] == INT32_MIN) { f[j] = 0.f; continue; }
+      int32_t biased = s[j] + 0x4B400000;
+      float sb;
+      memcpy(&sb, &biased, 4);
+      f[j] = (float)exp2((double)fmaf(sb, sc, nm));
+      ts += f[j];
+    }
+    l = l * alpha + ts;
+    float p8[64];
+    for (int j = 0; j < 64; ++j) p8[j] = lut[or_e4m3(f[j])];
+    for (int d = 0; d < D; ++d) {
+      const uint8_t* vr = vt + ((int64_t)kvh * D + d) * skv_pad + (int64_t)t * 64;
+      float pv = 0.f;
+      for (int j = 0; j < 64; ++j) pv += p8[j] * lut[vr[j]];
+      acc[d] = acc[d] * alpha + pv;
+    }
+  }
+  *m_io = m;
+  *l_io = l;
+}
+
+/* split_full / split_parts: the build's key-range split of the attention grid
+ * (units = (head, 256-query tile), unit index head * ceil(Sq/256) + row/256). Units
+ * at or past split_full run as split_parts ranges of key tiles, [j*nt/P, (j+1)*nt/P),
+ * each with its own m, l, acc, merged as M = max m_j, w_j = 2^(m_j - M),
+ * l = sum l_j w_j, acc = sum acc_j w_j in part order. split_parts <= 1: no split. */
 void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, const float* qs,
                      const float* ks, const float* vamax, int Sq, int Skv, int Hq, int Hkv, int D,
                      int64_t sq_pad, int64_t skv_pad, const uint8_t* kv_valid, const int* rows,
-                     int n_rows, float* out, int threads, float headroom) {
-  (void)Sq;
+                     int n_rows, float* out, int threads, float headroom, int split_full, int split_parts) {
   const int group = Hq / Hkv;
-  const float L448 = 8.807354922057604f;
+  const int ntq = (Sq + 255) / 256;
   float lut[256];
   for (int c = 0; c < 256; ++c) lut[c] = or_e4m3_to_f32((uint8_t)c);
 #ifdef _OPENMP
@@ -268,53 +328,31 @@ void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, cons
     int ri = (int)(job / Hq), head = (int)(job % Hq), row = rows[ri], kvh = head / group;
     const int8_t* qr = qi + ((int64_t)head * sq_pad + row) * D;
     const float qscale = qs[(int64_t)head * (sq_pad / 16) + row / 16];
-    float m = -INFINITY, l = 0.f;
-    float* acc = (float*)calloc(D, sizeof(float));
-    int32_t s[64];
-    float f[64];
+    const float* ksh = ks + (int64_t)kvh * (skv_pad / 64);
     const int ntiles = (int)((Skv + 63) / 64);
-    for (int t = 0; t < ntiles; ++t) {
-      const float sc = qscale * ks[(int64_t)kvh * (skv_pad / 64) + t];
-      int live_any = 0;
-      int32_t im = INT32_MIN;
-      for (int j = 0; j < 64; ++j) {
-        int64_t key = (int64_t)t * 64 + j;
-        int live = key < Skv && (!kv_valid || kv_valid[key]);
-        const int8_t* kr = ki + ((int64_t)kvh * skv_pad + key) * D;
-        int32_t dot = 0;
-        for (int d = 0; d < D; ++d) dot += (int32_t)qr[d] * (int32_t)kr[d];
-        s[j] = live ? dot : INT32_MIN;
-        if (live) { live_any = 1; if (dot > im) im = dot; }
-      }
-      if (!live_any) continue;
-      const float tmax = (float)im * sc;
-      /* headroom 0: next = max(m, tmax), the reference rule (:327). headroom H > 0:
-       * lazy max, m moves only when the tile max exceeds it by more than H, and P
-       * carries 2^-H so it stays <= 448 (this build's kernel uses H = 2). */
-      float next = tmax > m + headroom ? tmax : m;
-      float alpha = m == -INFINITY ? 0.f : (float)exp2((double)(m - next));
-      m = next;
-      /* exponent as the reference computes it (:331, :337): the int32 score is read as
-       * the float 12582912 + s through its bits (s + 0x4B400000), one FMA with
-       * nm = (log2 448 - H - next) - 12582912*sc (two float roundings). */
-      const float nm = (L448 - headroom - next) - 12582912.f * sc;
-      float ts = 0.f;
-      for (int j = 0; j < 64; ++j) {
-        if (s[j] == INT32_MIN) { f[j] = 0.f; continue; }
-        int32_t biased = s[j] + 0x4B400000;
-        float sb;
-        memcpy(&sb, &biased, 4);
-        f[j] = (float)exp2((double)fmaf(sb, sc, nm));
-        ts += f[j];
-      }
-      l = l * alpha + ts;
-      float p8[64];
-      for (int j = 0; j < 64; ++j) p8[j] = lut[or_e4m3(f[j])];
-      for (int d = 0; d < D; ++d) {
-        const uint8_t* vr = vt + ((int64_t)kvh * D + d) * skv_pad + (int64_t)t * 64;
-        float pv = 0.f;
-        for (int j = 0; j < 64; ++j) pv += p8[j] * lut[vr[j]];
-        acc[d] = acc[d] * alpha + pv;
+    const int unit = head * ntq + row / 256;
+    const int parts = split_parts > 1 && unit >= split_full ? split_parts : 1;
+    float* acc = (float*)calloc(D, sizeof(float));
+    float* pa = (float*)calloc((size_t)parts * D, sizeof(float));
+    float pm[8], pl[8];
+    for (int j = 0; j < parts; ++j) {
+      pm[j] = -INFINITY;
+      pl[j] = 0.f;
+      or_sage_range(qr, qscale, ki, vt, ksh, kvh, Skv, D, skv_pad, kv_valid, lut, headroom,
+                    (int)((int64_t)j * ntiles / parts), (int)((int64_t)(j + 1) * ntiles / parts), &pm[j], &pl[j],
+                    pa + (size_t)j * D);
+    }
+    float l = pl[0];
+    if (parts == 1) {
+      memcpy(acc, pa, sizeof(float) * D);
+    } else {
+      float mm = -INFINITY;
+      for (int j = 0; j < parts; ++j) mm = fmaxf(mm, pm[j]);
+      l = 0.f;
+      for (int j = 0; j < parts; ++j) {
+        const float w = mm == -INFINITY ? 0.f : (float)exp2((double)(pm[j] - mm));
+        l += pl[j] * w;
+        for (int d = 0; d < D; ++d) acc[d] += pa[(size_t)j * D + d] * w;
       }
     }
     float* o = out + ((int64_t)ri * Hq + head) * D;
@@ -322,6 +360,7 @@ void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, cons
       float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
       o[d] = acc[d] * vamax[kvh * D + d] * inv;
     }
+    free(pa);
     free(acc);
   }
 }

@@ -83,15 +83,18 @@ def test_workspace_and_layout():
     p = AttnParams(Sq=4352, Skv=4352, Hq=24, Hkv=24, D=128)
     L = sage_layout(p)
     assert L["sq_pad"] == 4352 and L["skv_pad"] == 4352
-    for name in ("qi", "ki", "vt", "qs", "ks", "km", "va", "part", "total"):
+    for name in ("qi", "ki", "vt", "qs", "ks", "km", "va", "part", "split", "cnt", "total"):
         assert L[name] % 256 == 0
     assert L["qi"] == 0 and L["ki"] == 24 * 4352 * 128 and L["vt"] == 2 * 24 * 4352 * 128
     assert flash_attn_fp8_workspace(p) == L["total"]
-    assert L["total"] < 45e6  # config 2 workspace ~ 40 MB
+    # config 2: ~40 MB, plus ~132 KB per split work-group when the device's CU count
+    # does not divide the 408-unit grid (none without a device)
+    assert L["total"] < 45e6 + 135e3 * L["split_units"] * L["split_parts"]
+    assert L["cnt"] - L["split"] >= 4 * 33792 * L["split_units"] * L["split_parts"]
     p2 = AttnParams(Sq=1000, Skv=77, Hq=4, Hkv=2, D=128)
     L2 = sage_layout(p2)
     assert L2["sq_pad"] == 1024 and L2["skv_pad"] == 128
-    order = [L2[n] for n in ("qi", "ki", "vt", "qs", "ks", "km", "va", "part", "total")]
+    order = [L2[n] for n in ("qi", "ki", "vt", "qs", "ks", "km", "va", "part", "split", "cnt", "total")]
     assert order == sorted(order)
     assert L2["ki"] - L2["qi"] >= 4 * 1024 * 128 and L2["vt"] - L2["ki"] >= 2 * 128 * 128
 

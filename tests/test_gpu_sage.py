@@ -116,8 +116,12 @@ def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
     g = _quantized(ws, p, L)
     rows = np.array(rows, np.int32)
     mk = None if mask is None else mask.cpu().numpy()
+    # the kernel balances its grid by splitting the last round's units by key range;
+    # the emulator follows the same plan
+    units = (S + 255) // 256 * H
     emu = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128,
-                              kv_valid=mk, rows=rows, headroom=oracle.KERNEL_HEADROOM)
+                              kv_valid=mk, rows=rows, headroom=oracle.KERNEL_HEADROOM,
+                              split=(units - L["split_units"], L["split_parts"]))
     ref_rule = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128,
                                    kv_valid=mk, rows=rows, headroom=0.0)
     exact = oracle.attention_f64(_bits(q), _bits(k), _bits(v), S, S, H, H, 128, kv_valid=mk, rows=rows)
@@ -210,3 +214,29 @@ def test_sage_mask_equals_compacted_keys(cuda):
     flash_attn_fp8(q, kc, vc, o2, p2, _ws(p2, cuda))
     torch.cuda.synchronize()
     assert cosine(_f32(o1), _f32(o2)) > 0.999
+
+
+def test_split_units_dead_parts_and_repeat(cuda):
+    """Key-range split of the grid's last round: a unit whose first parts see only
+    padded keys merges to the same result as exact attention over the valid keys,
+    and repeated calls on one workspace are bit-identical (the arrival counters
+    return to zero after every merge)."""
+    Sq, Skv, H = 1024, 4352, 2
+    q, k, v, qs, ks = _bias_inputs(Sq, Skv, H, H, 128, 0, 2.0, cuda, 77)
+    mask = torch.ones(Skv, dtype=torch.uint8, device=cuda)
+    mask[: Skv * 2 // 5] = 0  # the first 40 % of the keys: whole parts with no live key
+    p = AttnParams(Sq=Sq, Skv=Skv, Hq=H, Hkv=H, D=128, kv_valid=mask)
+    L = sage_layout(p)
+    print(f"split units {L['split_units']} parts {L['split_parts']}", flush=True)
+    assert L["split_units"] == 8 and L["split_parts"] >= 4  # 8 units on a 256-CU device
+    ws = _ws(p, cuda)
+    outs = []
+    for _ in range(3):
+        o = torch.empty_like(q)
+        flash_attn_fp8(q, k, v, o, p, ws)
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert all(torch.equal(outs[0].view(torch.int16), x.view(torch.int16)) for x in outs[1:])
+    exact = oracle.attention_f64(_bits(q), _bits(k), _bits(v), Sq, Skv, H, H, 128, kv_valid=mask.cpu().numpy())
+    got = _f32(outs[0]).reshape(exact.shape)
+    assert cosine(got, exact) >= 0.995 and rel_rms(got, exact) < 0.04

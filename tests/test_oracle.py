@@ -402,3 +402,44 @@ def test_head_norm_rope_sum_order_is_the_reference_shuffle_pattern(D):
         rstd = np.float32(1.0 / np.sqrt(np.float64(np.float32(ss / np.float32(D)) + np.float32(1e-5))))
         want = oracle.bf16_to_f32(oracle.f32_to_bf16((xb[s] * rstd).astype(np.float32)))
         assert np.array_equal(out[s, 0], want)
+
+
+def test_sage_split_merge_duplicated_keys_is_exact():
+    """Split merge pinned by an invariant: K/V = [X; X] split into two parts at the
+    copy boundary gives each part the (m, l, acc) of X alone, so the merge has
+    w = 1, l = 2 l_X, acc = 2 acc_X, and the output equals the unsplit output over X
+    bit for bit (doubling is exact). A wrong weight, a dropped part or l taken from one
+    part only breaks the equality."""
+    rng = np.random.default_rng(21)
+    Sq, n, H, D = 40, 192, 2, 128
+    q = _bf16_rand(rng, (Sq, H, D)); k = _bf16_rand(rng, (n, H, D)); v = _bf16_rand(rng, (n, H, D))
+    _, t = oracle.sage_reference(q, k, v, Sq, n, H, H, D, rows=np.zeros(0, np.int32))
+    ki2 = np.concatenate([t["ki"], t["ki"]], axis=1)
+    vt2 = np.concatenate([t["vt"], t["vt"]], axis=2)
+    ks2 = np.concatenate([t["ks"], t["ks"]], axis=1)
+    args = (t["qi"], t["ki"], t["vt"], t["qs"], t["ks"], t["va"], Sq, n, H, H, D)
+    one = oracle.sage_emulate(*args, headroom=oracle.KERNEL_HEADROOM)
+    two = oracle.sage_emulate(t["qi"], ki2, vt2, t["qs"], ks2, t["va"], Sq, 2 * n, H, H, D,
+                              headroom=oracle.KERNEL_HEADROOM, split=(0, 2))
+    assert np.array_equal(one, two)
+    # unsplit over [X; X]: the same softmax up to the running-max path, not bitwise
+    seq = oracle.sage_emulate(t["qi"], ki2, vt2, t["qs"], ks2, t["va"], Sq, 2 * n, H, H, D,
+                              headroom=oracle.KERNEL_HEADROOM)
+    assert cosine(seq, one) > 0.9999
+
+
+def test_sage_split_merge_one_live_part():
+    """A split unit whose other parts see only padded keys (m = -inf, l = 0) merges to
+    exactly the output of the part that holds the live keys, computed unsplit over
+    those keys."""
+    rng = np.random.default_rng(22)
+    Sq, Skv, H, D = 16, 256, 1, 128
+    q = _bf16_rand(rng, (Sq, H, D)); k = _bf16_rand(rng, (Skv, H, D)); v = _bf16_rand(rng, (Skv, H, D))
+    mask = np.zeros(Skv, np.uint8); mask[192:] = 1  # only the last of 4 parts is live
+    _, t = oracle.sage_reference(q, k, v, Sq, Skv, H, H, D, kv_valid=mask, rows=np.zeros(0, np.int32))
+    args = (t["qi"], t["ki"], t["vt"], t["qs"], t["ks"], t["va"], Sq, Skv, H, H, D)
+    seq = oracle.sage_emulate(*args, kv_valid=mask, headroom=oracle.KERNEL_HEADROOM)
+    split = oracle.sage_emulate(*args, kv_valid=mask, headroom=oracle.KERNEL_HEADROOM, split=(0, 4))
+    assert np.array_equal(seq, split)
+    none = oracle.sage_emulate(*args, kv_valid=np.zeros(Skv, np.uint8), split=(0, 4))
+    assert np.all(none == 0)
