@@ -138,8 +138,9 @@ def main() -> int:
     if args.only:
         return _only(args.only, args.steps)
 
-    from miroxen_amd import (AttnParams, flash_attn, flash_attn_fp8, flash_attn_fp8_workspace, sage_attend,
-                             sage_quantize, version)
+    from miroxen_amd import (ROPE_INTERLEAVED, ROPE_NONE, AttnParams, flash_attn, flash_attn_fp8,
+                             flash_attn_fp8_workspace, head_norm_rope, sage_attend, sage_quantize,
+                             sage_quantize_norm_rope, version)
     from miroxen_amd.synth import CONFIGS, attn_flops, make_inputs
 
     dev = torch.device("cuda:0")
@@ -178,6 +179,45 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(flop / (ms_main * 1e-3) / 1e12, 2), "peak": PEAK_FP8,
                      "unit": "TFLOP/s", "frac": round(flop / (ms_main * 1e-3) / 1e12 / PEAK_FP8, 4),
                      "traffic": _traffic("sage_attn_config3")},
+    }
+
+    # ---- head_norm_rope fused into the Sage prologue (config-3 shape, Qwen-Image-style
+    # interleaved RoPE over all 128 channels, per-head RMS-norm weights) ----
+    # The reference's DiT block runs head_norm_rope on q, k and v (v: a plain dense copy,
+    # ROPE_NONE) from the fused QKV projection, then the Sage prologue
+    # (src/models/minimax_h3/dit.cpp:210-212, :223); the fused entry reads the projection once.
+    g = torch.Generator(device=dev).manual_seed(33)
+    HD = H * D
+    t = torch.randn(S, 3 * HD, device=dev, generator=g).to(torch.bfloat16)
+    qw = torch.rand(D, device=dev, generator=g) + 0.5
+    kw = torch.rand(D, device=dev, generator=g) + 0.5
+    ang = (torch.rand(S, D // 2, device=dev, generator=g) * 2 - 1) * 3.14159
+    cs, sn = torch.cos(ang), torch.sin(ang)
+    qd, kd, vd = (torch.empty(S, HD, dtype=torch.bfloat16, device=dev) for _ in range(3))
+    pd = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=D, kv_valid=m3)
+    pr = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=D, q_stride=3 * HD, kv_stride=3 * HD, o_stride=HD, kv_valid=m3)
+    wsn = torch.empty(flash_attn_fp8_workspace(pr), dtype=torch.uint8, device=dev)
+    base = t.data_ptr()
+
+    def separate():
+        head_norm_rope(t, S, 3 * HD, 0, H, D, qw, 1e-6, cs, sn, D, ROPE_INTERLEAVED, qd)
+        head_norm_rope(t, S, 3 * HD, HD, H, D, kw, 1e-6, cs, sn, D, ROPE_INTERLEAVED, kd)
+        head_norm_rope(t, S, 3 * HD, 2 * HD, H, D, None, 0.0, None, None, 0, ROPE_NONE, vd)
+        sage_quantize(qd, kd, vd, pd, wsn)
+
+    ms_sep = _time(separate, args.steps, args.warmup, args.warm_seconds)
+    ms_fused = _time(lambda: sage_quantize_norm_rope(base, base + 2 * HD, base + 4 * HD, pr, qw, kw, 1e-6, cs, sn,
+                                                     D, ROPE_INTERLEAVED, wsn),
+                     args.steps, args.warmup, args.warm_seconds)
+    ms_nr = _time(lambda: head_norm_rope(t, S, 3 * HD, 0, H, D, qw, 1e-6, cs, sn, D, ROPE_INTERLEAVED, qd),
+                  args.steps, args.warmup, args.warm_seconds)
+    nr_bytes = 4.0 * S * HD  # read + write bf16 of one [S, H, D] tensor
+    sage["norm_rope_fused"] = {
+        "ms_separate": round(ms_sep, 4), "ms_fused": round(ms_fused, 4),
+        "speedup": round(ms_sep / ms_fused, 3),
+        "fused_gbs": round(pro_bytes / (ms_fused * 1e-3) / 1e9, 1),
+        "head_norm_rope_ms": round(ms_nr, 4), "head_norm_rope_gbs": round(nr_bytes / (ms_nr * 1e-3) / 1e9, 1),
+        "chain": "separate = head_norm_rope x3 (q, k, v) + sage_quantize; fused = sage_quantize_norm_rope",
     }
 
     traffic = _traffic("flash_bf16_config2")

@@ -88,6 +88,17 @@ inline void flash_attn_fp8(const bf16* q, const bf16* k, const bf16* v, bf16* o,
   detail::check(mx_flash_attn_fp8(q, k, v, o, &c, ws, s));
 }
 
+// Fused head_norm_rope(q), head_norm_rope(k) + flash_attn_fp8 (see mx_flash_attn_fp8_norm_rope):
+// q/k are the raw projections; q_norm/k_norm may be null; throws when the shape is
+// outside the quantized path (there is no fallback).
+inline void flash_attn_fp8_norm_rope(const bf16* q, const bf16* k, const bf16* v, bf16* o, const AttnParams& p,
+                                     const float* q_norm, const float* k_norm, float eps, const float* cos,
+                                     const float* sin, int rot, int mode, void* ws, hipStream_t s) {
+  const mx_attn_params c = detail::to_c(p);
+  const mx_qk_norm_rope n{q_norm, k_norm, eps, cos, sin, rot, mode};
+  detail::check(mx_flash_attn_fp8_norm_rope(q, k, v, o, &c, &n, ws, s));
+}
+
 // Reference: attn_reference, src/kernels/attention.h:37-38.
 inline void attn_reference(const bf16* q, const bf16* k, const bf16* v, bf16* o, const AttnParams& p,
                            hipStream_t s) {

@@ -122,6 +122,32 @@ enum { MX_ROPE_NONE = 0, MX_ROPE_INTERLEAVED = 1, MX_ROPE_HALF = 2 };
 int mx_head_norm_rope(const void* in, int64_t S, int64_t in_stride, int64_t col0, int H, int D, const float* norm_w,
                       float eps, const float* cos, const float* sin, int rot, int mode, void* out, void* stream);
 
+/* Fused head_norm_rope + Sage attention. No single reference counterpart: it
+ * replaces the sequence a DiT block runs before the quantized attention,
+ * head_norm_rope(q), head_norm_rope(k) (src/kernels/ops.h:37-41, e.g.
+ * src/models/minimax_h3/dit.cpp:210-211) then flash_attn_fp8 (attention.h:32-33),
+ * without writing the normalised Q and K: q and k are the raw projections (rows
+ * addressed by p's q_stride / kv_stride), each row gets the per-head RMS-norm
+ * (q_norm / k_norm, NULL = none) and RoPE of the first `rot` channels with
+ * cos/sin [row][rot/2] (Q row i uses table row i, K row j row j) and the bf16
+ * rounding of head_norm_rope, then the Sage prologue. The workspace is
+ * bit-identical to mx_head_norm_rope on q and k followed by mx_sage_quantize.
+ * Needs the quantized path (mx_flash_attn_fp8_ok; D = 128) and, for
+ * MX_ROPE_HALF, rot % 16 == 0: otherwise MX_E_UNSUPPORTED (there is no
+ * fallback: the normalised tensors do not exist). */
+typedef struct mx_qk_norm_rope {
+  const float* q_norm;
+  const float* k_norm;
+  float eps;
+  const float* cos;
+  const float* sin;
+  int rot, mode;
+} mx_qk_norm_rope;
+int mx_sage_quantize_norm_rope(const void* q, const void* k, const void* v, const mx_attn_params* p,
+                               const mx_qk_norm_rope* nr, void* ws, void* stream);
+int mx_flash_attn_fp8_norm_rope(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
+                                const mx_qk_norm_rope* nr, void* ws, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

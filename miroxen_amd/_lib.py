@@ -20,6 +20,7 @@ SYMBOLS = (
     "mx_flash_attn", "mx_flash_attn_fp8_workspace", "mx_flash_attn_fp8_supported",
     "mx_flash_attn_fp8_ok", "mx_flash_attn_fp8", "mx_attn_reference", "mx_sage_layout_of",
     "mx_sage_quantize", "mx_sage_attend", "mx_last_error", "mx_version", "mx_head_norm_rope",
+    "mx_sage_quantize_norm_rope", "mx_flash_attn_fp8_norm_rope",
 )
 
 
@@ -31,6 +32,12 @@ class CParams(ctypes.Structure):
         ("q_offset", ctypes.c_int), ("q_stride", ctypes.c_int64), ("kv_stride", ctypes.c_int64),
         ("o_stride", ctypes.c_int64), ("kv_valid", ctypes.c_void_p),
     ]
+
+
+class CNormRope(ctypes.Structure):
+    """mx_qk_norm_rope: per-head RMS-norm weights of Q and K, eps, RoPE tables and mode."""
+    _fields_ = [("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p), ("eps", ctypes.c_float),
+                ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p), ("rot", ctypes.c_int), ("mode", ctypes.c_int)]
 
 
 class CLayout(ctypes.Structure):
@@ -65,6 +72,8 @@ def load():
         "mx_version": ([], ctypes.c_char_p),
         "mx_head_norm_rope": ([vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, vp,
                                ctypes.c_float, vp, vp, ctypes.c_int, ctypes.c_int, vp, vp], ctypes.c_int),
+        "mx_sage_quantize_norm_rope": ([vp, vp, vp, P, ctypes.POINTER(CNormRope), vp, vp], ctypes.c_int),
+        "mx_flash_attn_fp8_norm_rope": ([vp, vp, vp, vp, P, ctypes.POINTER(CNormRope), vp, vp], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

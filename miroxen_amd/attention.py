@@ -132,5 +132,27 @@ def head_norm_rope(inp, S: int, in_stride: int, col0: int, H: int, D: int, norm_
                                              _addr(cos), _addr(sin), rot, mode, _addr(out), _stream(stream)))
 
 
+def _norm_rope(q_norm, k_norm, eps, cos, sin, rot, mode):
+    return _lib.CNormRope(_addr(q_norm), _addr(k_norm), eps, _addr(cos), _addr(sin), rot, mode)
+
+
+def sage_quantize_norm_rope(q, k, v, p: AttnParams, q_norm, k_norm, eps: float, cos, sin, rot: int, mode: int,
+                            ws, stream=None) -> None:
+    """head_norm_rope(q), head_norm_rope(k) and the Sage prologue in one pass: q and k are
+    the raw projections (p's strides), q_norm/k_norm fp32 [D] or None, cos/sin fp32
+    [rows, rot/2] indexed by token. The workspace equals head_norm_rope + sage_quantize's."""
+    c, n = p.c(), _norm_rope(q_norm, k_norm, eps, cos, sin, rot, mode)
+    _lib.check(_lib.load().mx_sage_quantize_norm_rope(_addr(q), _addr(k), _addr(v), ctypes.byref(c),
+                                                      ctypes.byref(n), _addr(ws), _stream(stream)))
+
+
+def flash_attn_fp8_norm_rope(q, k, v, o, p: AttnParams, q_norm, k_norm, eps: float, cos, sin, rot: int,
+                             mode: int, ws, stream=None) -> None:
+    """sage_quantize_norm_rope then the Sage attention kernel (no fallback path)."""
+    c, n = p.c(), _norm_rope(q_norm, k_norm, eps, cos, sin, rot, mode)
+    _lib.check(_lib.load().mx_flash_attn_fp8_norm_rope(_addr(q), _addr(k), _addr(v), _addr(o), ctypes.byref(c),
+                                                       ctypes.byref(n), _addr(ws), _stream(stream)))
+
+
 def version() -> str:
     return _lib.load().mx_version().decode()

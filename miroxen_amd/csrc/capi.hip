@@ -22,7 +22,7 @@ hipError_t launch_naive_attn(const uint16_t*, const uint16_t*, const uint16_t*, 
                              hipStream_t);
 mx_sage_layout sage_layout(const mx_attn_params&);
 hipError_t launch_sage_quantize(const uint16_t*, const uint16_t*, const uint16_t*, const mx_attn_params&, char*,
-                                hipStream_t);
+                                hipStream_t, const NormRope*);
 hipError_t launch_sage_attend(uint16_t*, const mx_attn_params&, const char*, hipStream_t);
 }  // namespace mxa
 
@@ -199,7 +199,7 @@ int mx_flash_attn_fp8(const void* q, const void* k, const void* v, void* o, cons
   if (!ws || !ok) return mx_flash_attn(q, k, v, o, p, stream);  // reference :491
   auto s = static_cast<hipStream_t>(stream);
   rc = hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                                            static_cast<const uint16_t*>(v), a, static_cast<char*>(ws), s),
+                                            static_cast<const uint16_t*>(v), a, static_cast<char*>(ws), s, nullptr),
                   "flash_attn_fp8 prologue");
   if (rc) return rc;
   return hip_status(mxa::launch_sage_attend(static_cast<uint16_t*>(o), a, static_cast<const char*>(ws), s),
@@ -216,8 +216,65 @@ int mx_sage_quantize(const void* q, const void* k, const void* v, const mx_attn_
   if (!ws) return fail(MX_E_INVALID, "sage_quantize: null workspace");
   return hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                                               static_cast<const uint16_t*>(v), a, static_cast<char*>(ws),
-                                              static_cast<hipStream_t>(stream)),
+                                              static_cast<hipStream_t>(stream), nullptr),
                     "sage_quantize");
+}
+
+// Fused head_norm_rope + Sage prologue: the head_norm_rope rules (reference
+// ops.cu:201) for the norm/rope block, the quantized path's rules for the rest.
+static int norm_rope_args(const mx_qk_norm_rope* nr, const mx_attn_params& a, const char* who,
+                          mxa::NormRope out[2]) {
+  if (!nr) return fail(MX_E_INVALID, "%s: null norm/rope block", who);
+  const int rot = nr->rot, mode = nr->mode;
+  if (!(rot >= 0 && rot <= a.D && rot % 2 == 0)) return fail(MX_E_INVALID, "%s: D=%d rot=%d", who, a.D, rot);
+  if (!(mode == MX_ROPE_NONE || mode == MX_ROPE_INTERLEAVED || mode == MX_ROPE_HALF))
+    return fail(MX_E_INVALID, "%s: unknown rope mode %d", who, mode);
+  if (mode != MX_ROPE_NONE && rot > 0 && (!nr->cos || !nr->sin))
+    return fail(MX_E_INVALID, "%s: rope needs cos and sin tables", who);
+  out[0] = mxa::NormRope{nr->q_norm, nr->eps, nr->cos, nr->sin, rot, mode};
+  out[1] = mxa::NormRope{nr->k_norm, nr->eps, nr->cos, nr->sin, rot, mode};
+  const int64_t rows = a.Sq > a.Skv ? a.Sq : a.Skv;
+  if (!mxa::nr128_supported(out[0], rows) || !mxa::nr128_supported(out[1], rows))
+    return fail(MX_E_UNSUPPORTED,
+                "%s: needs 16-byte aligned norm weights and rope tables, rot %% 8 == 0 (rotate-half: %% 16)", who);
+  return MX_OK;
+}
+
+int mx_sage_quantize_norm_rope(const void* q, const void* k, const void* v, const mx_attn_params* p,
+                               const mx_qk_norm_rope* nr, void* ws, void* stream) {
+  mx_attn_params a;
+  bool ok = false;
+  int rc = sage_args(q, k, v, q, p, ws, &a, &ok);
+  if (rc) return rc;
+  if (!ok) return fail(MX_E_UNSUPPORTED, "sage_quantize_norm_rope: arguments not supported by the quantized path");
+  if (!ws) return fail(MX_E_INVALID, "sage_quantize_norm_rope: null workspace");
+  mxa::NormRope n[2];
+  rc = norm_rope_args(nr, a, "sage_quantize_norm_rope", n);
+  if (rc) return rc;
+  return hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                              static_cast<const uint16_t*>(v), a, static_cast<char*>(ws),
+                                              static_cast<hipStream_t>(stream), n),
+                    "sage_quantize_norm_rope");
+}
+
+int mx_flash_attn_fp8_norm_rope(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
+                                const mx_qk_norm_rope* nr, void* ws, void* stream) {
+  mx_attn_params a;
+  bool ok = false;
+  int rc = sage_args(q, k, v, o, p, ws, &a, &ok);
+  if (rc) return rc;
+  if (!ok) return fail(MX_E_UNSUPPORTED, "flash_attn_fp8_norm_rope: arguments not supported by the quantized path");
+  if (!ws) return fail(MX_E_INVALID, "flash_attn_fp8_norm_rope: null workspace");
+  mxa::NormRope n[2];
+  rc = norm_rope_args(nr, a, "flash_attn_fp8_norm_rope", n);
+  if (rc) return rc;
+  auto s = static_cast<hipStream_t>(stream);
+  rc = hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                            static_cast<const uint16_t*>(v), a, static_cast<char*>(ws), s, n),
+                  "flash_attn_fp8_norm_rope prologue");
+  if (rc) return rc;
+  return hip_status(mxa::launch_sage_attend(static_cast<uint16_t*>(o), a, static_cast<const char*>(ws), s),
+                    "flash_attn_fp8_norm_rope");
 }
 
 int mx_sage_attend(void* o, const mx_attn_params* p, const void* ws, void* stream) {

@@ -35,6 +35,23 @@ __global__ void __launch_bounds__(256) head_norm_rope_kernel(const uint16_t* __r
   }
 }
 
+// D = 128: one row per 16 lanes (nr128_row), 16 rows per work-group, 16-byte
+// loads and stores. Requires 16-byte aligned rows (in, in_stride, col0, out).
+template <int MODE>
+__global__ void __launch_bounds__(256) head_norm_rope_d128(const uint16_t* __restrict__ in, int64_t S,
+                                                           int64_t in_stride, int64_t col0, int H, NormRope nr,
+                                                           uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t rowid = int64_t(blockIdx.x) * 16 + (threadIdx.x >> 4);  // = s * H + h
+  const bool valid = rowid < S * H;
+  const int64_t s = valid ? rowid / H : 0;
+  const int h = valid ? int(rowid % H) : 0;
+  float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (valid) load8_bf16(x, in + s * in_stride + col0 + int64_t(h) * 128 + 8 * (lane & 15));
+  nr128_row<MODE>(x, s, valid, nr, lane);
+  if (valid) *reinterpret_cast<u32x4*>(out + rowid * 128 + 8 * (lane & 15)) = pack8_bf16(x);
+}
+
 }  // namespace
 
 hipError_t launch_head_norm_rope(const uint16_t* in, int64_t S, int64_t in_stride, int64_t col0, int H, int D,
@@ -43,6 +60,17 @@ hipError_t launch_head_norm_rope(const uint16_t* in, int64_t S, int64_t in_strid
   const int64_t blocks = (rows + 3) / 4;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
   const dim3 grid{unsigned(blocks)}, block{256};
+  const bool a16 = (reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) % 16 == 0 &&
+                   in_stride % 8 == 0 && col0 % 8 == 0;
+  if (D == 128 && a16 && nr128_supported(nr, S)) {
+    const int64_t b16 = (rows + 15) / 16;
+    if (b16 > 0x7fffffff) return hipErrorInvalidValue;
+    const int m = nr128_mode(nr);
+    auto kern = m == kRopeNone ? head_norm_rope_d128<kRopeNone>
+              : m == kRopeInterleaved ? head_norm_rope_d128<kRopeInterleaved> : head_norm_rope_d128<kRopeHalf>;
+    hipLaunchKernelGGL(kern, dim3(unsigned(b16)), block, 0, s, in, S, in_stride, col0, H, nr, out);
+    return hipGetLastError();
+  }
   if (D <= 64) hipLaunchKernelGGL(head_norm_rope_kernel<1>, grid, block, 0, s, in, S, in_stride, col0, H, D, nr, out);
   else if (D <= 128) hipLaunchKernelGGL(head_norm_rope_kernel<2>, grid, block, 0, s, in, S, in_stride, col0, H, D, nr, out);
   else if (D <= 192) hipLaunchKernelGGL(head_norm_rope_kernel<3>, grid, block, 0, s, in, S, in_stride, col0, H, D, nr, out);

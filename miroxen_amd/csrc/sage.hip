@@ -11,6 +11,7 @@
 #include <type_traits>
 
 #include "attn_common.hpp"
+#include "norm_rope.hpp"
 
 
 namespace mxa {
@@ -49,10 +50,16 @@ __device__ __forceinline__ u32x2 quant8(const float (&x)[8], float inv) {
 
 constexpr int kStatChunk = 128;  // tokens staged in LDS per step of a stats block
 
+// NRM >= 0: q and k are the raw projections; every row gets the per-head RMS-norm
+// + RoPE of head_norm_rope (nq / nk, nr128_row with rope mode NRM) and its bf16
+// rounding on the way in, so the workspace is bit-identical to head_norm_rope
+// followed by the plain prologue. NRM = -1: the plain prologue.
+template <int NRM>
 __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                     const uint16_t* __restrict__ v, mx_attn_params p, int nb,
                                                     float qmult, int64_t sq_pad, float* __restrict__ part,
-                                                    int8_t* __restrict__ qi, float* __restrict__ qs) {
+                                                    int8_t* __restrict__ qi, float* __restrict__ qs, NormRope nq,
+                                                    NormRope nk) {
   __shared__ __align__(16) uint16_t kt[kStatChunk * D];
   __shared__ __align__(16) uint16_t vt_[kStatChunk * D];
   const int tid = threadIdx.x, nstat = p.Hkv * nb;
@@ -64,11 +71,39 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
     float sum = 0.f, am = 0.f;
     for (int64_t c0 = t0; c0 < t1; c0 += kStatChunk) {
       const int rows = int(t1 - c0 < kStatChunk ? t1 - c0 : kStatChunk);
-      for (int i = tid; i < rows * (D / 8); i += 256) {
-        const int r = i / (D / 8), c = (i % (D / 8)) * 8;
-        const int64_t g = (c0 + r) * p.kv_stride + int64_t(h) * D + c;
-        *reinterpret_cast<u32x4*>(&kt[r * D + c]) = *reinterpret_cast<const u32x4*>(k + g);
-        *reinterpret_cast<u32x4*>(&vt_[r * D + c]) = *reinterpret_cast<const u32x4*>(v + g);
+      if constexpr (NRM >= 0) {
+        // K rows normalised on the way into LDS: one row per 16 lanes, 16 per pass
+        // (all eight rows of a lane group loaded before any is normalised)
+        const int lane = tid & 63, c = (lane & 15) * 8;
+        constexpr int RPG = kStatChunk / 16;  // rows per 16-lane group
+        u32x4 raw[RPG];
+#pragma unroll
+        for (int u = 0; u < RPG; ++u) {
+          const int r = u * 16 + (tid >> 4);
+          raw[u] = u32x4{0, 0, 0, 0};
+          if (r < rows) raw[u] = *reinterpret_cast<const u32x4*>(k + (c0 + r) * p.kv_stride + int64_t(h) * D + c);
+        }
+#pragma unroll
+        for (int u = 0; u < RPG; ++u) {
+          const int r = u * 16 + (tid >> 4);
+          float x[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) x[j] = bf2f(uint16_t(raw[u][j >> 1] >> ((j & 1) * 16)));
+          nr128_row<NRM>(x, c0 + r, r < rows, nk, lane);
+          if (r < rows) *reinterpret_cast<u32x4*>(&kt[r * D + c]) = pack8_bf16(x);
+        }
+        for (int i = tid; i < rows * (D / 8); i += 256) {
+          const int r = i / (D / 8), cc = (i % (D / 8)) * 8;
+          *reinterpret_cast<u32x4*>(&vt_[r * D + cc]) =
+              *reinterpret_cast<const u32x4*>(v + (c0 + r) * p.kv_stride + int64_t(h) * D + cc);
+        }
+      } else {
+        for (int i = tid; i < rows * (D / 8); i += 256) {
+          const int r = i / (D / 8), c = (i % (D / 8)) * 8;
+          const int64_t g = (c0 + r) * p.kv_stride + int64_t(h) * D + c;
+          *reinterpret_cast<u32x4*>(&kt[r * D + c]) = *reinterpret_cast<const u32x4*>(k + g);
+          *reinterpret_cast<u32x4*>(&vt_[r * D + c]) = *reinterpret_cast<const u32x4*>(v + g);
+        }
       }
       __syncthreads();
       if (tid < D) {
@@ -92,17 +127,23 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
   if (gid >= int64_t(p.Hq) * ng) return;
   const int h = int(gid / ng), grp = int(gid % ng);
   float x[4][8], am = 0.f;
+  u32x4 raw[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int ci = lane + i * 64, r = ci >> 4, c = (ci & 15) * 8;
     const int64_t row = int64_t(grp) * 16 + r;
-    u32x4 raw = {0, 0, 0, 0};
-    if (row < p.Sq) raw = *reinterpret_cast<const u32x4*>(q + row * p.q_stride + int64_t(h) * D + c);
+    raw[i] = u32x4{0, 0, 0, 0};
+    if (row < p.Sq) raw[i] = *reinterpret_cast<const u32x4*>(q + row * p.q_stride + int64_t(h) * D + c);
+  }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      x[i][j] = bf2f(uint16_t(raw[j >> 1] >> ((j & 1) * 16)));
-      am = fmaxf(am, fabsf(x[i][j]));
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = int64_t(grp) * 16 + ((lane + i * 64) >> 4);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[i][j] = bf2f(uint16_t(raw[i][j >> 1] >> ((j & 1) * 16)));
+    // row r of the group on lanes 16(r&3) .. +15: the 16-lane layout of nr128_row
+    if constexpr (NRM >= 0) nr128_row<NRM>(x[i], row, row < p.Sq, nq, lane);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) am = fmaxf(am, fabsf(x[i][j]));
   }
   am = wave_max(am);
   const float inv = am > 0.f ? 127.f / am : 0.f;
@@ -155,11 +196,12 @@ __device__ __forceinline__ uint32_t e4m3x2_sat(float a, float b) {
 // Per (64-key tile, head): K - mean -> INT8 (one scale per tile) and V -> e4m3
 // transposed to [H][D][skv_pad] in natural key order. Thread tid owns channel
 // chunk tid%16 (8 channels) of rows tid/16 + 16*i, i = 0..3.
+template <int NRM>
 __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                      mx_attn_params p, int64_t skv_pad,
                                                      const float* __restrict__ km, const float* __restrict__ va,
                                                      int8_t* __restrict__ ki, float* __restrict__ ks,
-                                                     uint8_t* __restrict__ vt) {
+                                                     uint8_t* __restrict__ vt, NormRope nk) {
   __shared__ __align__(16) uint8_t tile[D][kKvPad + 16];
   __shared__ float red[4];
   const int h = blockIdx.y, k0 = blockIdx.x * kKvPad, tid = threadIdx.x;
@@ -186,10 +228,14 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
   float x[4][8], am = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const bool ok = k0 + r0 + 16 * i < p.Skv;
+    const int64_t row = k0 + r0 + 16 * i;
+    const bool ok = row < p.Skv;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[i][j] = bf2f(uint16_t(kraw[i][j >> 1] >> ((j & 1) * 16)));
+    if constexpr (NRM >= 0) nr128_row<NRM>(x[i], row, ok, nk, threadIdx.x & 63);  // row per 16 lanes
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      x[i][j] = ok ? bf2f(uint16_t(kraw[i][j >> 1] >> ((j & 1) * 16))) - mean[j] : 0.f;
+      x[i][j] = ok ? x[i][j] - mean[j] : 0.f;
       am = fmaxf(am, fabsf(x[i][j]));
     }
   }
@@ -665,8 +711,10 @@ mx_sage_layout sage_layout(const mx_attn_params& p) {
 
 // Prologue: preconditions checked by the caller (D == 128, q/k/v 16-byte aligned,
 // strides % 8 == 0, ws 256-byte aligned and large enough).
+// nr: null for the plain prologue, else {Q norm/rope, K norm/rope} applied on the fly
+// (D == 128 and nr128_supported, checked by the caller).
 hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint16_t* v, const mx_attn_params& p,
-                                char* ws, hipStream_t s) {
+                                char* ws, hipStream_t s, const NormRope* nr) {
   const mx_sage_layout L = sage_layout(p);
   const int nb = (p.Skv + kStatTok - 1) / kStatTok;
   float* part = reinterpret_cast<float*>(ws + L.part);
@@ -676,13 +724,20 @@ hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint
   const int64_t blocks1 = int64_t(p.Hkv) * nb + (qgroups + 3) / 4;
   if (blocks1 > 0x7fffffff) return hipErrorInvalidValue;
   const float qmult = p.scale * kLog2e;
-  hipLaunchKernelGGL(prep_stats_q, dim3(unsigned(blocks1)), dim3(256), 0, s, q, k, v, p, nb, qmult, L.sq_pad, part,
-                     reinterpret_cast<int8_t*>(ws + L.qi), reinterpret_cast<float*>(ws + L.qs));
+  const NormRope none{};
+  const NormRope nq = nr ? nr[0] : none, nk = nr ? nr[1] : none;
+  const int mode = nr ? nr128_mode(nq) : -1;
+  auto stats = mode < 0 ? prep_stats_q<-1> : mode == kRopeNone ? prep_stats_q<kRopeNone>
+             : mode == kRopeInterleaved ? prep_stats_q<kRopeInterleaved> : prep_stats_q<kRopeHalf>;
+  auto kvq = mode < 0 ? prep_kv_quant<-1> : mode == kRopeNone ? prep_kv_quant<kRopeNone>
+           : mode == kRopeInterleaved ? prep_kv_quant<kRopeInterleaved> : prep_kv_quant<kRopeHalf>;
+  hipLaunchKernelGGL(stats, dim3(unsigned(blocks1)), dim3(256), 0, s, q, k, v, p, nb, qmult, L.sq_pad, part,
+                     reinterpret_cast<int8_t*>(ws + L.qi), reinterpret_cast<float*>(ws + L.qs), nq, nk);
   hipLaunchKernelGGL(prep_finalize, dim3(p.Hkv), dim3(D), 0, s, p, nb, (const float*)part, km, va,
                      reinterpret_cast<int*>(ws + L.cnt), L.split_units);
-  hipLaunchKernelGGL(prep_kv_quant, dim3(unsigned(L.skv_pad / kKvPad), p.Hkv), dim3(256), 0, s, k, v, p, L.skv_pad,
+  hipLaunchKernelGGL(kvq, dim3(unsigned(L.skv_pad / kKvPad), p.Hkv), dim3(256), 0, s, k, v, p, L.skv_pad,
                      (const float*)km, (const float*)va, reinterpret_cast<int8_t*>(ws + L.ki),
-                     reinterpret_cast<float*>(ws + L.ks), reinterpret_cast<uint8_t*>(ws + L.vt));
+                     reinterpret_cast<float*>(ws + L.ks), reinterpret_cast<uint8_t*>(ws + L.vt), nk);
   return hipGetLastError();
 }
 
