@@ -103,6 +103,21 @@ def _only(which: str, n: int) -> int:
     p = AttnParams(Sq=cfg.S, Skv=cfg.S, Hq=cfg.H, Hkv=cfg.H, D=cfg.D, kv_valid=m)
     o = torch.empty_like(q)
     ws = torch.empty(flash_attn_fp8_workspace(p), dtype=torch.uint8, device=dev)
+    if which == "fused":  # fused norm/rope prologue on a [S, 3HD] projection (the bench's norm_rope_fused leg)
+        from miroxen_amd import ROPE_INTERLEAVED, sage_quantize_norm_rope
+        S, H, D = cfg.S, cfg.H, cfg.D
+        g = torch.Generator(device=dev).manual_seed(33)
+        t = torch.randn(S, 3 * H * D, device=dev, generator=g).to(torch.bfloat16)
+        qw, kw = torch.rand(D, device=dev, generator=g) + 0.5, torch.rand(D, device=dev, generator=g) + 0.5
+        ang = (torch.rand(S, D // 2, device=dev, generator=g) * 2 - 1) * 3.14159
+        cs, sn = torch.cos(ang), torch.sin(ang)
+        pr = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=D, q_stride=3 * H * D, kv_stride=3 * H * D, kv_valid=m)
+        wsr = torch.empty(flash_attn_fp8_workspace(pr), dtype=torch.uint8, device=dev)
+        b = t.data_ptr()
+        for _ in range(n):
+            sage_quantize_norm_rope(b, b + 2 * H * D, b + 4 * H * D, pr, qw, kw, 1e-6, cs, sn, D, ROPE_INTERLEAVED, wsr)
+        torch.cuda.synchronize()
+        return 0
     if which == "sage":
         sage_quantize(q, k, v, p, ws)
     for _ in range(n):
@@ -124,7 +139,7 @@ def main() -> int:
     ap.add_argument("--warm-seconds", type=float, default=0.5,
                     help="minimum seconds of untimed back-to-back calls before each timed region")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["bf16", "sage", "prologue", "copy"],
+    ap.add_argument("--only", choices=["bf16", "sage", "prologue", "fused", "copy"],
                     help="profiling driver: run just this kernel --steps times (no warm-up, no JSON); "
                          "'copy' is a 256 MiB device copy for calibrating HBM byte counters")
     args = ap.parse_args()
