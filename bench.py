@@ -139,6 +139,7 @@ def main() -> int:
     ap.add_argument("--warm-seconds", type=float, default=0.5,
                     help="minimum seconds of untimed back-to-back calls before each timed region")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--skip-large", action="store_true", help="skip configs 4 and 5 (S=12544, S=32760)")
     ap.add_argument("--only", choices=["bf16", "sage", "prologue", "fused", "copy"],
                     help="profiling driver: run just this kernel --steps times (no warm-up, no JSON); "
                          "'copy' is a 256 MiB device copy for calibrating HBM byte counters")
@@ -235,6 +236,28 @@ def main() -> int:
         "chain": "separate = head_norm_rope x3 (q, k, v) + sage_quantize; fused = sage_quantize_norm_rope",
     }
 
+    # ---- the other BASELINE configs at their full shapes (BF16 and Sage each) ----
+    others = {}
+    if not args.skip_large:
+        del q3, k3, v3, o3, ws, t, qd, kd, vd, wsn
+        for cid in (4, 5):
+            c = CONFIGS[cid]
+            qc, kc, vc, mc = make_inputs(c, seed=cid, device=dev)
+            pc = AttnParams(Sq=c.S, Skv=c.S, Hq=c.H, Hkv=c.H, D=c.D, kv_valid=mc)
+            oc = torch.empty_like(qc)
+            wc = torch.empty(flash_attn_fp8_workspace(pc), dtype=torch.uint8, device=dev)
+            fc = attn_flops(c.H, c.S, c.S, c.D)
+            n = max(3, args.steps // 20)
+            mb = _time(lambda: flash_attn(qc, kc, vc, oc, pc), n, args.warmup, args.warm_seconds)
+            me = _time(lambda: flash_attn_fp8(qc, kc, vc, oc, pc, wc), n, args.warmup, args.warm_seconds)
+            mk = _time(lambda: sage_attend(oc, pc, wc), n, args.warmup, args.warm_seconds)
+            others[f"config{cid}"] = {
+                "workload": c.name, "H": c.H, "S": c.S, "steps": n,
+                "bf16_ms": round(mb, 3), "bf16_tflops": round(fc / (mb * 1e-3) / 1e12, 1),
+                "sage_ms_end_to_end": round(me, 3), "sage_tflops_end_to_end": round(fc / (me * 1e-3) / 1e12, 1),
+                "sage_tflops_kernel": round(fc / (mk * 1e-3) / 1e12, 1)}
+            del qc, kc, vc, oc, wc
+
     traffic = _traffic("flash_bf16_config2")
     line = {
         "metric": "attention TFLOP/s + % MFMA peak at H=24,S=4352,D=128 (BF16 and Sage INT8/FP8)",
@@ -248,6 +271,7 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16, 4), "traffic": traffic},
         "sage": sage,
+        "other_configs": others,
         "timed_wall_s": round(wall, 3),
     }
     if not args.no_cpu:
