@@ -423,6 +423,94 @@ __device__ __forceinline__ void sage_load_k(const SageAddr& a, int tk, unsigned 
   });
 }
 
+// End of a work-group: a split part publishes (acc, m, l) and returns unless it is
+// the last of its unit to arrive, which merges every part; then O = acc * vamax[d] /
+// (448 l) -> bf16 for this lane's query row.
+__device__ __forceinline__ void sage_finish(f32x16 (&acc)[4], float m, float l, int part, int su, const SageSplit& sp,
+                                            int wave, int lane, int row, const mx_attn_params& p,
+                                            const float* __restrict__ va, int kvh, int head,
+                                            uint16_t* __restrict__ o) {
+  const int h = lane >> 5;
+  if (part >= 0) {
+    // Split unit: publish (acc, m, l), then the last part to arrive merges all parts.
+    // The partials move with device-scope (sc1) buffer accesses, which bypass the
+    // XCDs' non-coherent L2s for these lines only; a device-scope fence would write
+    // back and invalidate a whole L2 and with it every other work-group's K/V.
+    constexpr int kSc1 = 16;  // cache policy: device scope
+    const uint32_t unit_bytes = uint32_t(sp.parts) * kSplitFloats * 4;
+    const __amdgpu_buffer_rsrc_t rp = buf_rsrc(sp.part + int64_t(su) * sp.parts * kSplitFloats, unit_bytes);
+    const uint32_t lacc = uint32_t(wave * 16 * 64 + lane) * 16u;          // + j * 1024 for float4 j
+    const uint32_t lml = uint32_t(kSplitAcc + (wave * 64 + lane) * 2) * 4u;
+    const uint32_t mine = uint32_t(part) * kSplitFloats * 4u;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, f32x4{acc[db][g * 4], acc[db][g * 4 + 1], acc[db][g * 4 + 2], acc[db][g * 4 + 3]}),
+            rp, lacc + uint32_t(db * 4 + g) * 1024u, mine, kSc1);
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m, l}), rp, lml, mine, kSc1);
+    wait_vm();  // this lane's partial has reached the device-coherent level
+    __shared__ int last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int prev = __hip_atomic_fetch_add(sp.cnt + su, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = prev == sp.parts - 1;
+      if (last) __hip_atomic_store(sp.cnt + su, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+    }
+    __syncthreads();
+    if (!last) return;
+    // merge in part order (every part read back, this one's included, so the result
+    // does not depend on which part arrived last): M = max m_i, w_i = 2^(m_i - M),
+    // l = sum l_i w_i, acc = sum acc_i w_i
+    float mi[8], li[8];
+    float mm = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i >= sp.parts) break;
+      const f32x2 ml = __builtin_bit_cast(
+          f32x2, __builtin_amdgcn_raw_buffer_load_b64(rp, lml, uint32_t(i) * kSplitFloats * 4u, kSc1));
+      mi[i] = ml[0];
+      li[i] = ml[1];
+      mm = fmaxf(mm, ml[0]);
+    }
+    l = 0.f;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i >= sp.parts) break;
+      const float wi = mm == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(mi[i] - mm);
+      l += li[i] * wi;
+      f32x4 x[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        x[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rp, lacc + uint32_t(j) * 1024u, uint32_t(i) * kSplitFloats * 4u, kSc1));
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[j >> 2][(j & 3) * 4 + e] += x[j][e] * wi;
+    }
+  }
+  // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----
+  if (row < p.Sq) {
+    const float* vah = va + kvh * D;
+    const float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
+    uint16_t* dst = o + int64_t(row) * p.o_stride + head * D + h * 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + g * 8 + h * 4;
+        const f32x4 sv = *reinterpret_cast<const f32x4*>(vah + d);
+        uint32_t* d32 = reinterpret_cast<uint32_t*>(dst + db * 32 + g * 8);
+        d32[0] = pack_bf16x2(acc[db][g * 4] * sv[0] * inv, acc[db][g * 4 + 1] * sv[1] * inv);
+        d32[1] = pack_bf16x2(acc[db][g * 4 + 2] * sv[2] * inv, acc[db][g * 4 + 3] * sv[3] * inv);
+      }
+  }
+}
+
 template <int NS>
 __global__ void __launch_bounds__(512, 1)
 sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, const uint8_t* __restrict__ vt,
@@ -557,84 +645,7 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   }
 
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
-  if (part >= 0) {
-    // Split unit: publish (acc, m, l), then the last part to arrive merges all parts.
-    // The partials move with device-scope (sc1) buffer accesses, which bypass the
-    // XCDs' non-coherent L2s for these lines only; a device-scope fence would write
-    // back and invalidate a whole L2 and with it every other work-group's K/V.
-    constexpr int kSc1 = 16;  // cache policy: device scope
-    const uint32_t unit_bytes = uint32_t(sp.parts) * kSplitFloats * 4;
-    const __amdgpu_buffer_rsrc_t rp = buf_rsrc(sp.part + int64_t(su) * sp.parts * kSplitFloats, unit_bytes);
-    const uint32_t lacc = uint32_t(wave * 16 * 64 + lane) * 16u;          // + j * 1024 for float4 j
-    const uint32_t lml = uint32_t(kSplitAcc + (wave * 64 + lane) * 2) * 4u;
-    const uint32_t mine = uint32_t(part) * kSplitFloats * 4u;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(u32x4, f32x4{acc[db][g * 4], acc[db][g * 4 + 1], acc[db][g * 4 + 2], acc[db][g * 4 + 3]}),
-            rp, lacc + uint32_t(db * 4 + g) * 1024u, mine, kSc1);
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m, l}), rp, lml, mine, kSc1);
-    wait_vm();  // this lane's partial has reached the device-coherent level
-    __shared__ int last;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const int prev = __hip_atomic_fetch_add(sp.cnt + su, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = prev == sp.parts - 1;
-      if (last) __hip_atomic_store(sp.cnt + su, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
-    }
-    __syncthreads();
-    if (!last) return;
-    // merge in part order (every part read back, this one's included, so the result
-    // does not depend on which part arrived last): M = max m_i, w_i = 2^(m_i - M),
-    // l = sum l_i w_i, acc = sum acc_i w_i
-    float mi[8], li[8];
-    float mm = -__builtin_inff();
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (i >= sp.parts) break;
-      const f32x2 ml = __builtin_bit_cast(
-          f32x2, __builtin_amdgcn_raw_buffer_load_b64(rp, lml, uint32_t(i) * kSplitFloats * 4u, kSc1));
-      mi[i] = ml[0];
-      li[i] = ml[1];
-      mm = fmaxf(mm, ml[0]);
-    }
-    l = 0.f;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (i >= sp.parts) break;
-      const float wi = mm == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(mi[i] - mm);
-      l += li[i] * wi;
-      f32x4 x[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        x[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rp, lacc + uint32_t(j) * 1024u, uint32_t(i) * kSplitFloats * 4u, kSc1));
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[j >> 2][(j & 3) * 4 + e] += x[j][e] * wi;
-    }
-  }
-  // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----
-  if (row < p.Sq) {
-    const float* vah = va + kvh * D;
-    const float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
-    uint16_t* dst = o + int64_t(row) * p.o_stride + head * D + h * 4;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = db * 32 + g * 8 + h * 4;
-        const f32x4 sv = *reinterpret_cast<const f32x4*>(vah + d);
-        uint32_t* d32 = reinterpret_cast<uint32_t*>(dst + db * 32 + g * 8);
-        d32[0] = pack_bf16x2(acc[db][g * 4] * sv[0] * inv, acc[db][g * 4 + 1] * sv[1] * inv);
-        d32[1] = pack_bf16x2(acc[db][g * 4 + 2] * sv[2] * inv, acc[db][g * 4 + 3] * sv[3] * inv);
-      }
-  }
+  sage_finish(acc, m, l, part, su, sp, wave, lane, row, p, va, kvh, head, o);
 }
 
 }  // namespace
