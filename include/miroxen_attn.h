@@ -148,6 +148,32 @@ int mx_sage_quantize_norm_rope(const void* q, const void* k, const void* v, cons
 int mx_flash_attn_fp8_norm_rope(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
                                 const mx_qk_norm_rope* nr, void* ws, void* stream);
 
+/* ---- block-scaled GEMM (the DiT linears' low-precision path) ----
+ * Reference: src/kernels/blockscale.h:12-37 (QMode, QMat, qmode_supported,
+ * qdata_bytes, qscale_bytes, quantize_blockscaled, gemm_blockscaled; cuBLASLt in
+ * blockscale.cu:134-216). MX_QMODE_MXFP8: e4m3 data, one UE8M0 (power-of-two)
+ * scale per 32 K values, on gfx950's scaled MFMA. MX_QMODE_NVFP4 (e4m3 scales per
+ * 16 values + a per-tensor scale) has no gfx950 scaled-MFMA form: qmode_supported
+ * reports 0 and the caller keeps BF16, as the reference does on cards without it.
+ * Scale layout: sf[r * kbp + kb] with kbp = K/32 rounded up to 4, rows padded to
+ * 128 (the reference's qscale_bytes size; its cuBLASLt 128x4 interleave is not
+ * reproduced: only this library reads the scales). */
+enum { MX_QMODE_BF16 = 0, MX_QMODE_MXFP8 = 1, MX_QMODE_NVFP4 = 2 };
+int mx_qmode_supported(int mode, int device, int* supported);
+size_t mx_qdata_bytes(int mode, int64_t rows, int64_t K);
+size_t mx_qscale_bytes(int mode, int64_t rows, int64_t K);
+/* Reference quantize_blockscaled (blockscale.cu:113-131): x [rows, K] bf16 with row
+ * stride ldx -> q [rows, K] e4m3 (dense) and sf. K % 32 == 0, ldx % 8 == 0, x 16-byte
+ * aligned (reference MX_CHECK). amax is unused for MXFP8 (may be NULL). */
+int mx_quantize_blockscaled(int mode, const void* x, int64_t ldx, int64_t rows, int64_t K, void* q, void* sf,
+                            float* amax, void* stream);
+/* Reference gemm_blockscaled (blockscale.cu:134-216): Y[M, N] (bf16, row stride ldy)
+ * = X[M, K] W[N, K]^T (+ Y when beta == 1), both quantized with the same mode; beta
+ * must be 0 or 1. The reference's Ctx argument (cuBLASLt handle and workspace)
+ * becomes the stream: this kernel needs neither. */
+int mx_gemm_blockscaled(int mode, const void* wq, const void* wsf, const void* xq, const void* xsf, void* y,
+                        int64_t ldy, int64_t M, int64_t N, int64_t K, float beta, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

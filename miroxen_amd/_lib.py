@@ -21,6 +21,7 @@ SYMBOLS = (
     "mx_flash_attn_fp8_ok", "mx_flash_attn_fp8", "mx_attn_reference", "mx_sage_layout_of",
     "mx_sage_quantize", "mx_sage_attend", "mx_last_error", "mx_version", "mx_head_norm_rope",
     "mx_sage_quantize_norm_rope", "mx_flash_attn_fp8_norm_rope",
+    "mx_qmode_supported", "mx_qdata_bytes", "mx_qscale_bytes", "mx_quantize_blockscaled", "mx_gemm_blockscaled",
 )
 
 
@@ -74,6 +75,13 @@ def load():
                                ctypes.c_float, vp, vp, ctypes.c_int, ctypes.c_int, vp, vp], ctypes.c_int),
         "mx_sage_quantize_norm_rope": ([vp, vp, vp, P, ctypes.POINTER(CNormRope), vp, vp], ctypes.c_int),
         "mx_flash_attn_fp8_norm_rope": ([vp, vp, vp, vp, P, ctypes.POINTER(CNormRope), vp, vp], ctypes.c_int),
+        "mx_qmode_supported": ([ctypes.c_int, ctypes.c_int, ip], ctypes.c_int),
+        "mx_qdata_bytes": ([ctypes.c_int, ctypes.c_int64, ctypes.c_int64], ctypes.c_size_t),
+        "mx_qscale_bytes": ([ctypes.c_int, ctypes.c_int64, ctypes.c_int64], ctypes.c_size_t),
+        "mx_quantize_blockscaled": ([ctypes.c_int, vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, vp, vp, vp,
+                                     vp], ctypes.c_int),
+        "mx_gemm_blockscaled": ([ctypes.c_int, vp, vp, vp, vp, vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                 ctypes.c_int64, ctypes.c_float, vp], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

@@ -13,7 +13,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libmiroxen_attn.so")
-SOURCES = ["capi.hip", "flash_bf16.hip", "naive.hip", "norm_rope.hip", "sage.hip"]
+SOURCES = ["blockscale.hip", "capi.hip", "flash_bf16.hip", "naive.hip", "norm_rope.hip", "sage.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",

@@ -1,0 +1,306 @@
+// MXFP8 block-scaled GEMM for gfx950: quantizer + GEMM on the MX-scaled MFMA.
+// Reference: src/kernels/blockscale.{h,cu} (quantize_blockscaled :113-131,
+// quant_kernel MXFP8 branch :69-108, gemm_blockscaled :134-216 on cuBLASLt).
+//
+// Format (OCP MX, the reference's MXFP8): e4m3 data, one power-of-two scale (UE8M0)
+// per 32 consecutive K values of a row. gfx950's v_mfma_scale_f32_32x32x64_f8f6f4
+// consumes exactly that: lane half h supplies the UE8M0 scale of K block h of each
+// 64-value MFMA step (selected per operand by op_sel); see the operand layout note
+// in mxfp8_gemm.
+//
+// Scale layout (this build's, not cuBLASLt's 128x4 interleave): sf[r * kbp + kb],
+// kbp = K/32 rounded up to 4, rows padded to 128 (the reference's qscale_bytes size).
+// The quantizer writes 127 (= 1.0) into every padding byte, so padded K blocks and
+// rows contribute 0 (data 0 times a finite scale) instead of 0 x NaN (0xFF).
+//
+// GEMM (Y[M,N] bf16 = X[M,K] W[N,K]^T, both K-major): tiles of 256 n x 256 m per
+// 4-wave work-group, one wave per SIMD, each wave 128 n x 128 m = 4 x 4 MFMA blocks
+// of 32 x 32 (C = W X^T: lane = one m column, 16 n rows; the 256 fp32 accumulators
+// live in AGPRs). K advances in stages of 128 bytes DMA'd into LDS
+// (buffer_load ... lds, 1 KB per op, rows past the matrix read as zeros), double
+// buffered; LDS rows are 128 B with their 16-byte chunks XOR'd by (row >> 1) & 7, so
+// each 16-lane group of an operand read hits 16 distinct chunk slots.
+#include <type_traits>
+
+#include "attn_common.hpp"
+
+namespace mxa {
+
+namespace {
+
+constexpr int kMxBlock = 32;       // K values per UE8M0 scale
+constexpr int kTile = 256;         // n and m per work-group
+constexpr int kStage = 128;        // K bytes per LDS stage
+constexpr int kStageB = kTile * kStage;  // 32 KB per operand per stage
+
+__host__ __device__ inline int64_t pad_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// ---------------- quantizer ----------------
+// One thread per 32-value block of a row: bmax = max |x|; e = the smallest power of
+// two with bmax / 2^e <= 448 (frexp of bmax / 448: mantissa 0.5 -> e = ex - 1,
+// else ex; clamped to [-127, 127]; bmax = 0 -> -127); q = e4m3(x * 2^-e), round to
+// nearest even, saturate to +-448; scale byte e + 127 (reference :95-104).
+__global__ void __launch_bounds__(256) mxfp8_quant(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
+                                                   int64_t K, uint8_t* __restrict__ q, uint8_t* __restrict__ sf,
+                                                   int64_t kbp, int64_t rows_pad) {
+  const int64_t nkb = K / kMxBlock;
+  const int64_t id = int64_t(blockIdx.x) * 256 + threadIdx.x;  // over rows_pad * kbp
+  if (id >= rows_pad * kbp) return;
+  const int64_t r = id / kbp, kb = id % kbp;
+  if (r >= rows || kb >= nkb) {  // padding: scale 1.0
+    sf[id] = 127;
+    return;
+  }
+  const uint16_t* src = x + r * ldx + kb * kMxBlock;
+  float v[32];
+  float bmax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const u32x4 u = *reinterpret_cast<const u32x4*>(src + 8 * j);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      v[8 * j + t] = bf2f(uint16_t(u[t >> 1] >> ((t & 1) * 16)));
+      bmax = fmaxf(bmax, fabsf(v[8 * j + t]));
+    }
+  }
+  int e = -127;
+  if (bmax > 0.f) {
+    int ex;
+    const float mant = frexpf(bmax / 448.f, &ex);
+    e = mant == 0.5f ? ex - 1 : ex;
+    e = e < -127 ? -127 : (e > 127 ? 127 : e);
+  }
+  const float inv = exp2f(float(-e));
+  u32x4 w[2];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float a = __builtin_fminf(__builtin_fmaxf(v[4 * j] * inv, -448.f), 448.f);
+    float b = __builtin_fminf(__builtin_fmaxf(v[4 * j + 1] * inv, -448.f), 448.f);
+    float c = __builtin_fminf(__builtin_fmaxf(v[4 * j + 2] * inv, -448.f), 448.f);
+    float d = __builtin_fminf(__builtin_fmaxf(v[4 * j + 3] * inv, -448.f), 448.f);
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w[j >> 2][j & 3] = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
+  }
+  u32x4* dst = reinterpret_cast<u32x4*>(q + r * K + kb * kMxBlock);
+  dst[0] = w[0];
+  dst[1] = w[1];
+  sf[id] = uint8_t(e + 127);
+}
+
+// ---------------- GEMM ----------------
+// One operand's DMA of stage k0: 32 ops of 1 KB (8 rows x 128 B each); wave w
+// issues ops j = 4 * jj + w. Lane i of op j fills physical chunk i % 8 of row
+// 8 j + i / 8, i.e. logical chunk (i % 8) ^ ((row >> 1) & 7); ((row >> 1) & 7)
+// depends on j only through its parity, so a lane keeps two offsets.
+struct OpAddr {
+  uint32_t lo[2];  // per-lane byte offsets (row-in-op * K + logical chunk * 16) for even / odd j
+  uint32_t chunk[2];  // logical chunk * 16 (for the K-tail check)
+};
+__device__ __forceinline__ OpAddr op_addr(int64_t K, int lane) {
+  OpAddr a;
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int rin = lane >> 3, p = lane & 7;
+    const int row = 8 * par + rin;  // row modulo 16 is what the swizzle sees
+    const int c = p ^ ((row >> 1) & 7);
+    a.chunk[par] = uint32_t(c * 16);
+    a.lo[par] = uint32_t(rin) * uint32_t(K) + uint32_t(c * 16);
+  }
+  return a;
+}
+
+template <bool KTAIL>
+__device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rs, const OpAddr& a, int64_t K, int k0,
+                                          unsigned char* dst, int wave) {
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) {
+    const int j = 4 * jj + wave;
+    uint32_t off = a.lo[j & 1];
+    if constexpr (KTAIL)
+      if (uint32_t(k0) + a.chunk[j & 1] >= uint32_t(K)) off = 0x80000000u;  // past K: read as zeros
+    buf2lds16(rs, off, uint32_t(8 * j) * uint32_t(K) + uint32_t(k0), (MXA_LDS void*)(dst + j * 1024));
+  }
+}
+
+__global__ void __launch_bounds__(256, 1)
+mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, const uint8_t* __restrict__ xq,
+           const uint8_t* __restrict__ xsf, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int beta,
+           int ntn) {
+  __shared__ __align__(16) unsigned char a0[kStageB], a1[kStageB], b0[kStageB], b1[kStageB];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int tn = L % ntn, tm = L / ntn;
+  const int n0 = tn * kTile, m0 = tm * kTile;
+  const int wn = (wave & 1) * 128, wm = (wave >> 1) * 128;
+  const int kbp = int(pad_up(K / kMxBlock, 4));
+  const int nst = (K + kStage - 1) / kStage;
+  const bool ktail = K % kStage != 0;
+
+  const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wq + int64_t(n0) * K, uint32_t(int64_t(N - n0) * K));
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xq + int64_t(m0) * K, uint32_t(int64_t(M - m0) * K));
+  const OpAddr oa = op_addr(K, lane);
+  // scales: one u32 (4 K blocks = one stage) per (lane, row block); rows past the
+  // 128-padded matrix read as zeros (their data is zero too)
+  const int n = lane & 31, h = lane >> 5;
+  const __amdgpu_buffer_rsrc_t rsw = buf_rsrc(wsf, uint32_t(pad_up(N, 128) * kbp));
+  const __amdgpu_buffer_rsrc_t rsx = buf_rsrc(xsf, uint32_t(pad_up(M, 128) * kbp));
+  uint32_t sw_off[4], sx_off[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    sw_off[b] = uint32_t(n0 + wn + b * 32 + n) * uint32_t(kbp);
+    sx_off[b] = uint32_t(m0 + wm + b * 32 + n) * uint32_t(kbp);
+  }
+  auto scales = [&](int st, uint32_t (&sa)[4], uint32_t (&sb)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t ra = __builtin_amdgcn_raw_buffer_load_b32(rsw, sw_off[b] + uint32_t(st * 4), 0, 0);
+      const uint32_t rb = __builtin_amdgcn_raw_buffer_load_b32(rsx, sx_off[b] + uint32_t(st * 4), 0, 0);
+      // byte 0: K block 2s + h of step s = 0, byte 2: of step s = 1 (op_sel 0 / 2)
+      sa[b] = (ra >> (8 * h)) & 0x00FF00FFu;
+      sb[b] = (rb >> (8 * h)) & 0x00FF00FFu;
+    }
+  };
+
+  // LDS operand reads: rows row0 + n of an operand tile for K step s. In the f8
+  // operand of the 32x32x64 MFMA, bytes 0-15 of lane half h are K 16h .. 16h+15 and
+  // bytes 16-31 are K 32 + 16h ..; the UE8M0 scale of lane half h applies to K block
+  // h (K 32h .. 32h+31, i.e. bytes 0-15 of both halves for h = 0, bytes 16-31 for
+  // h = 1). So lane half h takes logical chunks 4s + h (K block 2s) and 4s + 2 + h
+  // (K block 2s + 1), and its scale is that of K block 2s + h. The per-lane part of
+  // the address is one base plus the chunk offsets; the row block is a constant.
+  const int x = (n >> 1) & 7;
+  int coff[4];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    coff[2 * s] = ((4 * s + h) ^ x) << 4;
+    coff[2 * s + 1] = ((4 * s + 2 + h) ^ x) << 4;
+  }
+  const int abase = (wn + n) * kStage, bbase = (wm + n) * kStage;
+  auto opread = [&](const unsigned char* base, int b, int s) __attribute__((always_inline)) -> i32x8 {
+    const unsigned char* rp = base + b * 32 * kStage;
+    const i32x4 lo = *reinterpret_cast<const i32x4*>(rp + coff[2 * s]);
+    const i32x4 hi = *reinterpret_cast<const i32x4*>(rp + coff[2 * s + 1]);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  if (nst == 1 && ktail) {
+    dma_stage<true>(rw, oa, K, 0, a0, wave_u);
+    dma_stage<true>(rx, oa, K, 0, b0, wave_u);
+  } else {
+    dma_stage<false>(rw, oa, K, 0, a0, wave_u);
+    dma_stage<false>(rx, oa, K, 0, b0, wave_u);
+  }
+  uint32_t sa[4], sb[4];
+  scales(0, sa, sb);
+
+  auto stage = [&](int st, const unsigned char* ca, const unsigned char* cb, unsigned char* na,
+                   unsigned char* nb) __attribute__((always_inline)) {
+    wait_vm();     // this wave's DMA of stage st (and its scale loads) landed ...
+    block_sync();  // ... for every wave; the other buffers were last read in stage st-1
+    uint32_t ta[4], tb[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) ta[b] = sa[b], tb[b] = sb[b];
+    if (st + 1 < nst) {
+      const int k1 = (st + 1) * kStage;
+      if (ktail && st + 2 == nst) {
+        dma_stage<true>(rw, oa, K, k1, na, wave_u);
+        dma_stage<true>(rx, oa, K, k1, nb, wave_u);
+      } else {
+        dma_stage<false>(rw, oa, K, k1, na, wave_u);
+        dma_stage<false>(rx, oa, K, k1, nb, wave_u);
+      }
+      scales(st + 1, sa, sb);
+    }
+    auto kstep = [&](auto sc) __attribute__((always_inline)) {
+      constexpr int S = decltype(sc)::value;
+      i32x8 av[4], bv[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        av[b] = opread(ca + abase, b, S);
+        bv[b] = opread(cb + bbase, b, S);
+        // operands stay in VGPRs: the 256 accumulators fill the AGPR file
+        asm volatile("" : "+v"(av[b]), "+v"(bv[b]));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[i], bv[j], acc[i][j], 0, 0, 2 * S,
+                                                                       int(ta[i]), 2 * S, int(tb[j]));
+    };
+    kstep(std::integral_constant<int, 0>{});
+    kstep(std::integral_constant<int, 1>{});
+  };
+  for (int st = 0; st < nst; st += 2) {
+    stage(st, a0, b0, a1, b1);
+    if (st + 1 < nst) stage(st + 1, a1, b1, a0, b0);
+  }
+  wait_vm();  // no LDS-DMA may land after the work-group ends
+
+  // epilogue: C[n][m] -> Y[m][n]; lane column m, rows n = 8g + 4h + (0..3) per block.
+  // One m block at a time, one row pointer per block, compile-time n offsets.
+  const bool vec = (reinterpret_cast<uintptr_t>(y) & 7) == 0 && ldy % 4 == 0;
+  const int nl = n0 + wn + 4 * h;  // this lane's first n
+#pragma unroll 1
+  for (int j = 0; j < 4; ++j) {
+    const int m = m0 + wm + j * 32 + n;
+    if (m >= M) continue;
+    uint16_t* rowp = y + int64_t(m) * ldy + nl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int off = i * 32 + 8 * g;
+        float v4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v4[e] = acc[i][j][4 * g + e];
+        if (vec && nl + off + 3 < N) {
+          u32x2* d2 = reinterpret_cast<u32x2*>(rowp + off);
+          if (beta) {
+            const u32x2 old = *d2;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] += bf2f(uint16_t(old[e >> 1] >> ((e & 1) * 16)));
+          }
+          *d2 = u32x2{pack_bf16x2(v4[0], v4[1]), pack_bf16x2(v4[2], v4[3])};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (nl + off + e < N) rowp[off + e] = f2bf(beta ? v4[e] + bf2f(rowp[off + e]) : v4[e]);
+        }
+      }
+  }
+}
+
+}  // namespace
+
+size_t mx_qscale_size(int64_t rows, int64_t K) { return size_t(pad_up(rows, 128) * pad_up(K / kMxBlock, 4)); }
+
+hipError_t launch_mxfp8_quant(const uint16_t* x, int64_t ldx, int64_t rows, int64_t K, uint8_t* q, uint8_t* sf,
+                              hipStream_t s) {
+  const int64_t kbp = pad_up(K / kMxBlock, 4), rp = pad_up(rows, 128);
+  const int64_t blocks = (rp * kbp + 255) / 256;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(mxfp8_quant, dim3(unsigned(blocks)), dim3(256), 0, s, x, ldx, rows, K, q, sf, kbp, rp);
+  return hipGetLastError();
+}
+
+// Preconditions (checked by the caller): K % 32 == 0, (N + 255) / 256 * 256 * K < 2^31,
+// same for M; beta 0 or 1.
+hipError_t launch_mxfp8_gemm(const uint8_t* wq, const uint8_t* wsf, const uint8_t* xq, const uint8_t* xsf,
+                             uint16_t* y, int64_t ldy, int M, int N, int K, int beta, hipStream_t s) {
+  const int ntn = (N + kTile - 1) / kTile, ntm = (M + kTile - 1) / kTile;
+  const int64_t blocks = int64_t(ntn) * ntm;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(mxfp8_gemm, dim3(unsigned(blocks)), dim3(256), 0, s, wq, wsf, xq, xsf, y, ldy, M, N, K, beta,
+                     ntn);
+  return hipGetLastError();
+}
+
+}  // namespace mxa

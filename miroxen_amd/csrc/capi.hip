@@ -24,6 +24,10 @@ mx_sage_layout sage_layout(const mx_attn_params&);
 hipError_t launch_sage_quantize(const uint16_t*, const uint16_t*, const uint16_t*, const mx_attn_params&, char*,
                                 hipStream_t, const NormRope*);
 hipError_t launch_sage_attend(uint16_t*, const mx_attn_params&, const char*, hipStream_t);
+size_t mx_qscale_size(int64_t rows, int64_t K);
+hipError_t launch_mxfp8_quant(const uint16_t*, int64_t, int64_t, int64_t, uint8_t*, uint8_t*, hipStream_t);
+hipError_t launch_mxfp8_gemm(const uint8_t*, const uint8_t*, const uint8_t*, const uint8_t*, uint16_t*, int64_t, int,
+                             int, int, int, hipStream_t);
 }  // namespace mxa
 
 namespace {
@@ -307,6 +311,66 @@ int mx_head_norm_rope(const void* in, int64_t S, int64_t in_stride, int64_t col0
   return hip_status(mxa::launch_head_norm_rope(static_cast<const uint16_t*>(in), S, in_stride, col0, H, D, nr,
                                                static_cast<uint16_t*>(out), static_cast<hipStream_t>(stream)),
                     "head_norm_rope");
+}
+
+int mx_qmode_supported(int mode, int device, int* supported) {
+  if (!supported) return fail(MX_E_INVALID, "qmode_supported: null output");
+  if (mode != MX_QMODE_BF16 && mode != MX_QMODE_MXFP8 && mode != MX_QMODE_NVFP4)
+    return fail(MX_E_INVALID, "qmode_supported: unknown mode %d", mode);
+  if (mode == MX_QMODE_BF16) return *supported = 1, MX_OK;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess) return hip_status(e, "qmode_supported");
+  if (device < 0 || device >= count) return fail(MX_E_INVALID, "qmode_supported: no device %d", device);
+  *supported = mode == MX_QMODE_MXFP8 && device_is_gfx950(device) ? 1 : 0;
+  return MX_OK;
+}
+
+size_t mx_qdata_bytes(int mode, int64_t rows, int64_t K) {
+  if (rows <= 0 || K <= 0) return 0;
+  return size_t(rows) * size_t(K) / (mode == MX_QMODE_NVFP4 ? 2 : 1);
+}
+
+size_t mx_qscale_bytes(int mode, int64_t rows, int64_t K) {
+  if (rows <= 0 || K <= 0) return 0;
+  const int64_t vec = mode == MX_QMODE_NVFP4 ? 16 : 32;
+  return size_t((rows + 127) / 128 * 128) * size_t((K / vec + 3) / 4 * 4);
+}
+
+int mx_quantize_blockscaled(int mode, const void* x, int64_t ldx, int64_t rows, int64_t K, void* q, void* sf,
+                            float* amax, void* stream) {
+  (void)amax;
+  if (mode == MX_QMODE_BF16) return fail(MX_E_INVALID, "quantize_blockscaled: bf16 is not a quantized mode");
+  if (mode != MX_QMODE_MXFP8) return fail(MX_E_UNSUPPORTED, "quantize_blockscaled: only MXFP8 on gfx950");
+  // reference MX_CHECK, blockscale.cu:116
+  if (!(K % 32 == 0 && ldx % 8 == 0 && aligned(x, 16)))
+    return fail(MX_E_INVALID, "quantize_blockscaled: need K%%32==0, ldx%%8==0, 16B-aligned input");
+  if (rows == 0) return MX_OK;
+  if (rows < 0 || K <= 0 || ldx < K || !x || !q || !sf || !aligned(q, 16))
+    return fail(MX_E_INVALID, "quantize_blockscaled: bad tensor arguments");
+  return hip_status(mxa::launch_mxfp8_quant(static_cast<const uint16_t*>(x), ldx, rows, K, static_cast<uint8_t*>(q),
+                                            static_cast<uint8_t*>(sf), static_cast<hipStream_t>(stream)),
+                    "quantize_blockscaled");
+}
+
+int mx_gemm_blockscaled(int mode, const void* wq, const void* wsf, const void* xq, const void* xsf, void* y,
+                        int64_t ldy, int64_t M, int64_t N, int64_t K, float beta, void* stream) {
+  if (M == 0 || N == 0) return MX_OK;  // reference :136
+  if (!(beta == 0.f || beta == 1.f)) return fail(MX_E_INVALID, "gemm_blockscaled: beta must be 0 or 1");
+  if (mode != MX_QMODE_MXFP8) return fail(MX_E_UNSUPPORTED, "gemm_blockscaled: only MXFP8 on gfx950");
+  if (M < 0 || N < 0 || K <= 0 || K % 32 || ldy < N || !wq || !wsf || !xq || !xsf || !y || !aligned(wq, 16) ||
+      !aligned(xq, 16) || !aligned(wsf, 4) || !aligned(xsf, 4) || !aligned(y, 2))
+    return fail(MX_E_INVALID, "gemm_blockscaled: bad arguments (M=%lld N=%lld K=%lld)", (long long)M, (long long)N,
+                (long long)K);
+  // 32-bit buffer offsets within a 256-row tile's operand, and int grid coordinates
+  if ((N + 255) / 256 * 256 * K >= (int64_t(1) << 31) || (M + 255) / 256 * 256 * K >= (int64_t(1) << 31) ||
+      M > 0x7fffffff || N > 0x7fffffff)
+    return fail(MX_E_UNSUPPORTED, "gemm_blockscaled: matrix too large for 32-bit offsets");
+  return hip_status(mxa::launch_mxfp8_gemm(static_cast<const uint8_t*>(wq), static_cast<const uint8_t*>(wsf),
+                                           static_cast<const uint8_t*>(xq), static_cast<const uint8_t*>(xsf),
+                                           static_cast<uint16_t*>(y), ldy, int(M), int(N), int(K), beta == 1.f ? 1 : 0,
+                                           static_cast<hipStream_t>(stream)),
+                    "gemm_blockscaled");
 }
 
 }  // extern "C"

@@ -59,6 +59,10 @@ def lib():
                                       _p, _p, _i, _p, _i, _f, _i, _i]
         L.or_head_norm_rope.restype = None
         L.or_head_norm_rope.argtypes = [_p, _i64, _i64, _i64, _i, _i, _p, _f, _p, _p, _i, _i, _p]
+        L.or_mxfp8_quantize.restype = None
+        L.or_mxfp8_quantize.argtypes = [_p, _i64, _i64, _i64, _p, _p]
+        L.or_gemm_mxfp8.restype = None
+        L.or_gemm_mxfp8.argtypes = [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i]
         L.or_num_threads.restype = _i
         _lib = L
     return _lib
@@ -189,3 +193,23 @@ def head_norm_rope(inp, S, in_stride, col0, H, D, norm_w=None, eps=0.0, cos=None
     lib().or_head_norm_rope(_ptr(inp), S, in_stride, col0, H, D, _ptr(nw), float(eps), _ptr(cs), _ptr(sn),
                             rot, mode, _ptr(out))
     return out
+
+
+def mxfp8_quantize(x, rows, K, ldx=0):
+    """MXFP8 quantizer (reference blockscale.cu:69-108): x bf16 bits [rows, ldx] ->
+    (q uint8 [rows, K] e4m3, sf uint8 [rows, K/32] UE8M0)."""
+    x = _c(x, np.uint16)
+    ldx = ldx or K
+    q = np.zeros((rows, K), np.uint8)
+    sf = np.zeros((rows, K // 32), np.uint8)
+    lib().or_mxfp8_quantize(_ptr(x), ldx, rows, K, _ptr(q), _ptr(sf))
+    return q, sf
+
+
+def gemm_mxfp8(wq, wsf, xq, xsf, M, N, K, threads=0):
+    """Y[M, N] = deq(X) deq(W)^T in float64 (returned as float32)."""
+    wq = _c(wq, np.uint8); wsf = _c(wsf, np.uint8); xq = _c(xq, np.uint8); xsf = _c(xsf, np.uint8)
+    out = np.zeros((M, N), np.float32)
+    lib().or_gemm_mxfp8(_ptr(wq), _ptr(wsf), _ptr(xq), _ptr(xsf), M, N, K, _ptr(out), threads)
+    return out
+

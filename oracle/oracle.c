@@ -436,3 +436,58 @@ int or_num_threads(void) {
   return 1;
 #endif
 }
+
+/* ---------- MXFP8 block-scaled quantizer (reference src/kernels/blockscale.cu:69-108) ----------
+ * Per row r and 32-value block kb of x (bf16, row stride ldx): bmax = max |v|;
+ * e = -127 when bmax == 0, else frexpf(bmax / 448.f) = mant * 2^ex and e = ex - 1
+ * when mant == 0.5 (bmax / 448 a power of two), ex otherwise, clamped to [-127, 127]
+ * (:95-101): the smallest power of two with bmax / 2^e <= 448. q = e4m3 SATFINITE of
+ * v * 2^-e (:102-103, the exact power of two the reference's exp2f(-e) returns),
+ * scale byte e + 127. q [rows][K] dense; sf [rows][K/32] (this library's layout). */
+void or_mxfp8_quantize(const uint16_t* x, int64_t ldx, int64_t rows, int64_t K, uint8_t* q, uint8_t* sf) {
+  const int64_t nkb = K / 32;
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t kb = 0; kb < nkb; ++kb) {
+      float v[32], bmax = 0.f;
+      for (int j = 0; j < 32; ++j) {
+        v[j] = or_bf16_to_f32(x[r * ldx + kb * 32 + j]);
+        if (fabsf(v[j]) > bmax) bmax = fabsf(v[j]);
+      }
+      int e = -127;
+      if (bmax > 0.f) {
+        int ex;
+        const float t = bmax / 448.f;
+        const float mant = frexpf(t, &ex);
+        e = mant == 0.5f ? ex - 1 : ex;
+        e = e < -127 ? -127 : (e > 127 ? 127 : e);
+      }
+      const float inv = ldexpf(1.f, -e);
+      for (int j = 0; j < 32; ++j) q[r * K + kb * 32 + j] = or_e4m3(v[j] * inv);
+      sf[r * nkb + kb] = (uint8_t)(e + 127);
+    }
+}
+
+/* Y[m][n] = sum_k deq(X[m][k]) * deq(W[n][k]) in double, deq(c) = e4m3(c) * 2^(s - 127)
+ * with s the block's scale byte (sf [rows][K/32]); out [M][N] as float. */
+void or_gemm_mxfp8(const uint8_t* wq, const uint8_t* wsf, const uint8_t* xq, const uint8_t* xsf, int64_t M,
+                   int64_t N, int64_t K, float* out, int threads) {
+  const int64_t nkb = K / 32;
+  float lut[256];
+  for (int c = 0; c < 256; ++c) lut[c] = or_e4m3_to_f32((uint8_t)c);
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) {
+      double acc = 0.0;
+      for (int64_t kb = 0; kb < nkb; ++kb) {
+        double blk = 0.0;
+        for (int j = 0; j < 32; ++j)
+          blk += (double)lut[xq[m * K + kb * 32 + j]] * (double)lut[wq[n * K + kb * 32 + j]];
+        acc += blk * ldexp(1.0, (int)xsf[m * nkb + kb] - 127) * ldexp(1.0, (int)wsf[n * nkb + kb] - 127);
+      }
+      out[m * N + n] = (float)acc;
+    }
+}
+

@@ -1,0 +1,82 @@
+"""GPU parity of the MXFP8 block-scaled quantizer and GEMM (mx_quantize_blockscaled /
+mx_gemm_blockscaled through the C ABI) against the oracle's restatement of the
+reference (src/kernels/blockscale.cu:69-108 quantizer, :134-216 GEMM contract):
+quantized bytes and scales bit-exact, the GEMM within bf16 rounding of the float64
+product of the dequantized operands."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from miroxen_amd.blockscale import (QMat, QMode, gemm_blockscaled, qdata_bytes, qmode_supported, qscale_bytes,
+                                    quantize_blockscaled)
+
+pytestmark = pytest.mark.gpu
+
+
+def _quant(x, rows, K, cuda, ldx=None):
+    ldx = ldx or K
+    q = torch.zeros(qdata_bytes(QMode.MXFP8, rows, K) + 64, dtype=torch.uint8, device=cuda)
+    sf = torch.full((qscale_bytes(QMode.MXFP8, rows, K),), 0xFF, dtype=torch.uint8, device=cuda)
+    quantize_blockscaled(QMode.MXFP8, x, ldx, rows, K, QMat(q, sf))
+    return q, sf
+
+
+def _sf_view(sf, rows, K):
+    kbp = (K // 32 + 3) // 4 * 4
+    return sf.cpu().numpy().reshape(-1, kbp)[:rows, : K // 32]
+
+
+def test_modes(cuda):
+    assert qmode_supported(QMode.BF16) and qmode_supported(QMode.MXFP8)
+    assert not qmode_supported(QMode.NVFP4)  # no e4m3-scaled MFMA on gfx950: callers keep BF16
+
+
+@pytest.mark.parametrize("rows,K,pad", [(1, 32, 0), (300, 256, 8), (129, 4096, 0), (2048, 3072, 0)])
+def test_quantizer_bit_exact(cuda, rows, K, pad):
+    print(f"mxfp8 quant rows={rows} K={K} pad={pad}", flush=True)
+    rng = np.random.default_rng(rows + K)
+    ldx = K + pad
+    xf = (rng.standard_normal((rows, ldx)) * np.exp2(rng.integers(-12, 12, (rows, 1)))).astype(np.float32)
+    xf[0, :32] = 0.0
+    xb = oracle.f32_to_bf16(xf)
+    x = torch.from_numpy(xb.view(np.int16)).to(cuda)
+    q, sf = _quant(x, rows, K, cuda, ldx)
+    torch.cuda.synchronize()
+    wq, ws = oracle.mxfp8_quantize(xb, rows, K, ldx)
+    assert np.array_equal(q.cpu().numpy()[: rows * K].reshape(rows, K), wq)
+    assert np.array_equal(_sf_view(sf, rows, K), ws)
+    assert np.all(q.cpu().numpy()[rows * K:] == 0), "wrote past the data"
+    # padding scale bytes hold 1.0 (127), so padded blocks contribute 0 x 1 in the GEMM
+    kbp = (K // 32 + 3) // 4 * 4
+    full = sf.cpu().numpy().reshape(-1, kbp)
+    assert np.all(full[rows:] == 127) and np.all(full[:, K // 32:] == 127)
+
+
+@pytest.mark.parametrize("M,N,K,beta", [
+    (256, 256, 128, 0.0), (300, 200, 96, 0.0), (77, 513, 4096, 1.0), (1024, 768, 3072, 0.0), (33, 31, 160, 1.0),
+])
+def test_gemm_matches_oracle(cuda, M, N, K, beta):
+    print(f"mxfp8 gemm M={M} N={N} K={K} beta={beta}", flush=True)
+    rng = np.random.default_rng(M * 7 + N + K)
+    xb = oracle.f32_to_bf16((rng.standard_normal((M, K)) * 2).astype(np.float32))
+    wb = oracle.f32_to_bf16((rng.standard_normal((N, K)) * 0.05).astype(np.float32))
+    to = lambda a: torch.from_numpy(a.view(np.int16)).to(cuda)
+    xq, xs = _quant(to(xb), M, K, cuda)
+    wq, ws = _quant(to(wb), N, K, cuda)
+    ldy = N + 8
+    y0 = oracle.f32_to_bf16(rng.standard_normal((M, ldy)).astype(np.float32))
+    y = to(y0).clone()
+    gemm_blockscaled(QMode.MXFP8, QMat(wq, ws), QMat(xq, xs), y, ldy, M, N, K, beta)
+    torch.cuda.synchronize()
+    got = oracle.bf16_to_f32(y.cpu().numpy().view(np.uint16)).astype(np.float64)
+    oq, os_ = oracle.mxfp8_quantize(xb, M, K)
+    owq, ows = oracle.mxfp8_quantize(wb, N, K)
+    want = oracle.gemm_mxfp8(owq, ows, oq, os_, M, N, K).astype(np.float64)
+    if beta:
+        want = want + oracle.bf16_to_f32(y0)[:, :N].astype(np.float64)
+    g = got[:, :N]
+    # fp32 accumulation then one bf16 rounding (plus the bf16 of Y for beta = 1)
+    tol = np.abs(want) * 2.0 ** -7 + np.abs(want).max() * 2.0 ** -14
+    assert np.all(np.abs(g - want) <= tol), float(np.max(np.abs(g - want) - tol))
+    np.testing.assert_array_equal(got[:, N:], oracle.bf16_to_f32(y0)[:, N:])  # columns past N untouched

@@ -443,3 +443,59 @@ def test_sage_split_merge_one_live_part():
     assert np.array_equal(seq, split)
     none = oracle.sage_emulate(*args, kv_valid=np.zeros(Skv, np.uint8), split=(0, 4))
     assert np.all(none == 0)
+
+
+# ---------------- MXFP8 block-scaled quantizer / GEMM (reference src/kernels/blockscale.cu) ----------------
+
+def _e4m3_table():
+    return np.array([oracle.e4m3_to_f32(c) for c in range(256)], np.float64)
+
+
+def test_mxfp8_quantizer_scale_rule_and_exact_values():
+    """Scale = the smallest power of two with bmax / 2^e <= 448 (checked against float64
+    log2, independent of the frexp formulation), padding of the rule's edge cases, and
+    blocks whose values are e4m3 numbers times 2^k round-trip exactly."""
+    rng = np.random.default_rng(31)
+    rows, K = 6, 256
+    x = (rng.standard_normal((rows, K)) * np.exp2(rng.integers(-20, 20, (rows, 1)))).astype(np.float32)
+    x[0, :32] = 0.0                                     # zero block -> e = -127, q = 0
+    x[1, :32] = 0.0; x[1, 5] = 448.0 * 2.0 ** 3         # bmax / 448 a power of two -> e = 3, q = 448
+    x[1, 32:64] = 0.0; x[1, 40] = -448.0 * 2.0 ** -5 * 1.0078125  # just above -> e = -4
+    t = _e4m3_table()
+    x[2, :32] = t[rng.integers(1, 0x7E, 32)] * 2.0 ** 7  # exact e4m3 values x 2^7
+    xb = oracle.f32_to_bf16(x)
+    q, sf = oracle.mxfp8_quantize(xb, rows, K)
+    xf = oracle.bf16_to_f32(xb).astype(np.float64)
+    bmax = np.abs(xf.reshape(rows, K // 32, 32)).max(-1)
+    with np.errstate(divide="ignore"):
+        want = np.where(bmax > 0, np.ceil(np.log2(bmax / 448.0)), -127).clip(-127, 127)
+    assert np.array_equal(sf.astype(np.int64) - 127, want.astype(np.int64))
+    assert sf[0, 0] == 0 and np.all(q[0, :32] == 0)
+    assert sf[1, 0] == 127 + 3 and q[1, 5] == 0x7E
+    assert sf[1, 1] == 127 - 4
+    deq = t[q].reshape(rows, K // 32, 32) * np.exp2(sf.astype(np.float64) - 127)[..., None]
+    np.testing.assert_array_equal(deq.reshape(rows, K)[2, :32], xf[2, :32])
+    # nearest-even rounding to the e4m3 grid of the block: error <= half an e4m3 ulp
+    err = np.abs(deq.reshape(rows, K) - xf)
+    scale = np.exp2(sf.astype(np.float64) - 127).repeat(32, axis=1)
+    assert np.all(err <= np.maximum(np.abs(xf) * 2.0 ** -4, scale * 2.0 ** -10) * (1 + 1e-12))
+
+
+def test_mxfp8_gemm_oracle_matches_numpy():
+    """The GEMM oracle against a numpy float64 restatement (dequantize, matmul), and the
+    identity: W = I with unit scales returns the dequantized X."""
+    rng = np.random.default_rng(32)
+    M, N, K = 7, 5, 96
+    xb = oracle.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32) * 3)
+    wb = oracle.f32_to_bf16(rng.standard_normal((N, K)).astype(np.float32) * 0.1)
+    xq, xs = oracle.mxfp8_quantize(xb, M, K)
+    wq, ws = oracle.mxfp8_quantize(wb, N, K)
+    t = _e4m3_table()
+    dq = lambda q, s: (t[q].reshape(q.shape[0], -1, 32) * np.exp2(s.astype(np.float64) - 127)[..., None]).reshape(q.shape)
+    want = dq(xq, xs) @ dq(wq, ws).T
+    got = oracle.gemm_mxfp8(wq, ws, xq, xs, M, N, K)
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-9)
+    eye = np.zeros((K, K), np.uint8); eye[np.arange(K), np.arange(K)] = 0x38  # e4m3 1.0
+    ones = np.full((K, K // 32), 127, np.uint8)
+    got = oracle.gemm_mxfp8(eye, ones, xq, xs, M, K, K)
+    np.testing.assert_array_equal(got, dq(xq, xs).astype(np.float32))
