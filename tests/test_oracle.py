@@ -447,7 +447,7 @@ def test_sage_split_merge_one_live_part():
 
 # ---------------- MXFP8 block-scaled quantizer / GEMM (reference src/kernels/blockscale.cu) ----------------
 
-def _e4m3_table():
+def _e4m3_lut():
     return np.array([oracle.e4m3_to_f32(c) for c in range(256)], np.float64)
 
 
@@ -461,7 +461,7 @@ def test_mxfp8_quantizer_scale_rule_and_exact_values():
     x[0, :32] = 0.0                                     # zero block -> e = -127, q = 0
     x[1, :32] = 0.0; x[1, 5] = 448.0 * 2.0 ** 3         # bmax / 448 a power of two -> e = 3, q = 448
     x[1, 32:64] = 0.0; x[1, 40] = -448.0 * 2.0 ** -5 * 1.0078125  # just above -> e = -4
-    t = _e4m3_table()
+    t = _e4m3_lut()
     x[2, :32] = t[rng.integers(1, 0x7E, 32)] * 2.0 ** 7  # exact e4m3 values x 2^7
     xb = oracle.f32_to_bf16(x)
     q, sf = oracle.mxfp8_quantize(xb, rows, K)
@@ -490,7 +490,7 @@ def test_mxfp8_gemm_oracle_matches_numpy():
     wb = oracle.f32_to_bf16(rng.standard_normal((N, K)).astype(np.float32) * 0.1)
     xq, xs = oracle.mxfp8_quantize(xb, M, K)
     wq, ws = oracle.mxfp8_quantize(wb, N, K)
-    t = _e4m3_table()
+    t = _e4m3_lut()
     dq = lambda q, s: (t[q].reshape(q.shape[0], -1, 32) * np.exp2(s.astype(np.float64) - 127)[..., None]).reshape(q.shape)
     want = dq(xq, xs) @ dq(wq, ws).T
     got = oracle.gemm_mxfp8(wq, ws, xq, xs, M, N, K)
