@@ -151,14 +151,13 @@ mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, cons
     sw_off[b] = uint32_t(n0 + wn + b * 32 + n) * uint32_t(kbp);
     sx_off[b] = uint32_t(m0 + wm + b * 32 + n) * uint32_t(kbp);
   }
-  auto scales = [&](int st, uint32_t (&sa)[4], uint32_t (&sb)[4]) __attribute__((always_inline)) {
+  // raw scale words of stage st (K blocks 4 st .. 4 st + 3), loaded a stage ahead
+  // and unpacked only after the next stage's wait, so no stage waits on their latency
+  auto scales = [&](int st, uint32_t (&ra)[4], uint32_t (&rb)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const uint32_t ra = __builtin_amdgcn_raw_buffer_load_b32(rsw, sw_off[b] + uint32_t(st * 4), 0, 0);
-      const uint32_t rb = __builtin_amdgcn_raw_buffer_load_b32(rsx, sx_off[b] + uint32_t(st * 4), 0, 0);
-      // byte 0: K block 2s + h of step s = 0, byte 2: of step s = 1 (op_sel 0 / 2)
-      sa[b] = (ra >> (8 * h)) & 0x00FF00FFu;
-      sb[b] = (rb >> (8 * h)) & 0x00FF00FFu;
+      ra[b] = __builtin_amdgcn_raw_buffer_load_b32(rsw, sw_off[b] + uint32_t(st * 4), 0, 0);
+      rb[b] = __builtin_amdgcn_raw_buffer_load_b32(rsx, sx_off[b] + uint32_t(st * 4), 0, 0);
     }
   };
 
@@ -204,9 +203,10 @@ mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, cons
                    unsigned char* nb) __attribute__((always_inline)) {
     wait_vm();     // this wave's DMA of stage st (and its scale loads) landed ...
     block_sync();  // ... for every wave; the other buffers were last read in stage st-1
+    // byte 0: K block 2s + h of step s = 0, byte 2: of step s = 1 (op_sel 0 / 2)
     uint32_t ta[4], tb[4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) ta[b] = sa[b], tb[b] = sb[b];
+    for (int b = 0; b < 4; ++b) ta[b] = (sa[b] >> (8 * h)) & 0x00FF00FFu, tb[b] = (sb[b] >> (8 * h)) & 0x00FF00FFu;
     if (st + 1 < nst) {
       const int k1 = (st + 1) * kStage;
       if (ktail && st + 2 == nst) {
