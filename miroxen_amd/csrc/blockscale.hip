@@ -32,6 +32,7 @@ constexpr int kMxBlock = 32;       // K values per UE8M0 scale
 constexpr int kTile = 256;         // n and m per work-group
 constexpr int kStage = 128;        // K bytes per LDS stage
 constexpr int kStageB = kTile * kStage;  // 32 KB per operand per stage
+constexpr int kGroupM = 4;               // tile rows per launch-order group
 
 __host__ __device__ inline int64_t pad_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
@@ -91,46 +92,52 @@ __global__ void __launch_bounds__(256) mxfp8_quant(const uint16_t* __restrict__ 
 // One operand's DMA of stage k0: 32 ops of 1 KB (8 rows x 128 B each); wave w
 // issues ops j = 4 * jj + w. Lane i of op j fills physical chunk i % 8 of row
 // 8 j + i / 8, i.e. logical chunk (i % 8) ^ ((row >> 1) & 7); ((row >> 1) & 7)
-// depends on j only through its parity, so a lane keeps two offsets.
+// depends on j only through its parity, which is the wave's. Both operands have
+// row stride K, so one set of 8 per-lane offsets serves both and the only
+// scalar offset is k0.
 struct OpAddr {
-  uint32_t lo[2];  // per-lane byte offsets (row-in-op * K + logical chunk * 16) for even / odd j
-  uint32_t chunk[2];  // logical chunk * 16 (for the K-tail check)
+  uint32_t vo[8];  // row (8 j + lane / 8) * K + logical chunk * 16, j = 4 jj + wave
+  uint32_t chunk;  // logical chunk * 16 (for the K-tail check)
 };
-__device__ __forceinline__ OpAddr op_addr(int64_t K, int lane) {
+__device__ __forceinline__ OpAddr op_addr(int64_t K, int lane, int wave) {
   OpAddr a;
+  const int rin = lane >> 3, p = lane & 7;
+  const int row = 8 * (wave & 1) + rin;  // row modulo 16 is what the swizzle sees
+  const int c = p ^ ((row >> 1) & 7);
+  a.chunk = uint32_t(c * 16);
 #pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    const int rin = lane >> 3, p = lane & 7;
-    const int row = 8 * par + rin;  // row modulo 16 is what the swizzle sees
-    const int c = p ^ ((row >> 1) & 7);
-    a.chunk[par] = uint32_t(c * 16);
-    a.lo[par] = uint32_t(rin) * uint32_t(K) + uint32_t(c * 16);
-  }
+  for (int jj = 0; jj < 8; ++jj) a.vo[jj] = uint32_t(8 * (4 * jj + wave) + rin) * uint32_t(K) + a.chunk;
   return a;
 }
 
 template <bool KTAIL>
 __device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rs, const OpAddr& a, int64_t K, int k0,
                                           unsigned char* dst, int wave) {
+  const bool past = KTAIL && uint32_t(k0) + a.chunk >= uint32_t(K);
 #pragma unroll
   for (int jj = 0; jj < 8; ++jj) {
     const int j = 4 * jj + wave;
-    uint32_t off = a.lo[j & 1];
-    if constexpr (KTAIL)
-      if (uint32_t(k0) + a.chunk[j & 1] >= uint32_t(K)) off = 0x80000000u;  // past K: read as zeros
-    buf2lds16(rs, off, uint32_t(8 * j) * uint32_t(K) + uint32_t(k0), (MXA_LDS void*)(dst + j * 1024));
+    const uint32_t off = past ? 0x80000000u : a.vo[jj];  // past K: read as zeros
+    buf2lds16(rs, off, uint32_t(k0), (MXA_LDS void*)(dst + j * 1024));
   }
 }
 
 __global__ void __launch_bounds__(256, 1)
 mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, const uint8_t* __restrict__ xq,
            const uint8_t* __restrict__ xsf, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int beta,
-           int ntn) {
-  __shared__ __align__(16) unsigned char a0[kStageB], a1[kStageB], b0[kStageB], b1[kStageB];
+           int ntn, int ntm) {
+  __shared__ __align__(16) unsigned char lds[4 * kStageB];
+  // stage buffers: operand A at lds + (st % 2) * kStageB, operand B 64 KB above it
+  unsigned char *const a0 = lds, *const a1 = lds + kStageB, *const b0 = lds + 2 * kStageB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int tn = L % ntn, tm = L / ntn;
+  // grouped order: consecutive tiles walk kGroupM tile rows (m) before moving
+  // along n, so the 32 concurrent tiles of one XCD (one L2) form a 4 x 8 block
+  // and share 12 operand strips instead of 33
+  const int gsz = kGroupM * ntn, grp = L / gsz, fm = grp * kGroupM;
+  const int gm = min(ntm - fm, kGroupM), li = L - grp * gsz;
+  const int tm = fm + li % gm, tn = li / gm;
   const int n0 = tn * kTile, m0 = tm * kTile;
   const int wn = (wave & 1) * 128, wm = (wave >> 1) * 128;
   const int kbp = int(pad_up(K / kMxBlock, 4));
@@ -139,7 +146,7 @@ mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, cons
 
   const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wq + int64_t(n0) * K, uint32_t(int64_t(N - n0) * K));
   const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xq + int64_t(m0) * K, uint32_t(int64_t(M - m0) * K));
-  const OpAddr oa = op_addr(K, lane);
+  const OpAddr oa = op_addr(K, lane, wave_u);
   // scales: one u32 (4 K blocks = one stage) per (lane, row block); rows past the
   // 128-padded matrix read as zeros (their data is zero too)
   const int n = lane & 31, h = lane >> 5;
@@ -187,94 +194,147 @@ mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, cons
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-
-  if (nst == 1 && ktail) {
-    dma_stage<true>(rw, oa, K, 0, a0, wave_u);
-    dma_stage<true>(rx, oa, K, 0, b0, wave_u);
-  } else {
-    dma_stage<false>(rw, oa, K, 0, a0, wave_u);
-    dma_stage<false>(rx, oa, K, 0, b0, wave_u);
-  }
-  uint32_t sa[4], sb[4];
-  scales(0, sa, sb);
-
-  auto stage = [&](int st, const unsigned char* ca, const unsigned char* cb, unsigned char* na,
-                   unsigned char* nb) __attribute__((always_inline)) {
-    wait_vm();     // this wave's DMA of stage st (and its scale loads) landed ...
-    block_sync();  // ... for every wave; the other buffers were last read in stage st-1
-    // byte 0: K block 2s + h of step s = 0, byte 2: of step s = 1 (op_sel 0 / 2)
-    uint32_t ta[4], tb[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) ta[b] = (sa[b] >> (8 * h)) & 0x00FF00FFu, tb[b] = (sb[b] >> (8 * h)) & 0x00FF00FFu;
-    if (st + 1 < nst) {
-      const int k1 = (st + 1) * kStage;
-      if (ktail && st + 2 == nst) {
-        dma_stage<true>(rw, oa, K, k1, na, wave_u);
-        dma_stage<true>(rx, oa, K, k1, nb, wave_u);
-      } else {
-        dma_stage<false>(rw, oa, K, k1, na, wave_u);
-        dma_stage<false>(rx, oa, K, k1, nb, wave_u);
-      }
-      scales(st + 1, sa, sb);
+    for (int j = 0; j < 4; ++j) {
+      // opaque zeros: left as constants, the register allocator splits the
+      // accumulators' live ranges at the loop header and spills them
+      acc[i][j] = f32x16{};
+      asm volatile("" : "+a"(acc[i][j]));
     }
-    auto kstep = [&](auto sc) __attribute__((always_inline)) {
-      constexpr int S = decltype(sc)::value;
-      i32x8 av[4], bv[4];
+
+  // DMA of stage st (operands and the raw scale words) into buffers (da, db)
+  auto fetch = [&](int st, unsigned char* da, unsigned char* db, uint32_t (&ra)[4],
+                   uint32_t (&rb)[4]) __attribute__((always_inline)) {
+    if (ktail && st + 1 == nst) {
+      dma_stage<true>(rw, oa, K, st * kStage, da, wave_u);
+      dma_stage<true>(rx, oa, K, st * kStage, db, wave_u);
+    } else {
+      dma_stage<false>(rw, oa, K, st * kStage, da, wave_u);
+      dma_stage<false>(rx, oa, K, st * kStage, db, wave_u);
+    }
+    scales(st, ra, rb);
+  };
+  // byte 0: K block 2s + h of step s = 0, byte 2: of step s = 1 (op_sel 0 / 2)
+  auto unpack = [&](const uint32_t (&ra)[4], const uint32_t (&rb)[4], uint32_t (&ta)[4],
+                    uint32_t (&tb)[4]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        av[b] = opread(ca + abase, b, S);
-        bv[b] = opread(cb + bbase, b, S);
-        // operands stay in VGPRs: the 256 accumulators fill the AGPR file
-        asm volatile("" : "+v"(av[b]), "+v"(bv[b]));
-      }
+    for (int b = 0; b < 4; ++b) ta[b] = (ra[b] >> (8 * h)) & 0x00FF00FFu, tb[b] = (rb[b] >> (8 * h)) & 0x00FF00FFu;
+  };
+  auto rd = [&](const unsigned char* ca, const unsigned char* cb, auto sc, i32x8 (&av)[4],
+                i32x8 (&bv)[4]) __attribute__((always_inline)) {
+    constexpr int S = decltype(sc)::value;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int b = 0; b < 4; ++b) {
+      av[b] = opread(ca + abase, b, S);
+      bv[b] = opread(cb + bbase, b, S);
+    }
+  };
+  // operands stay in VGPRs (the 256 accumulators fill the AGPR file); the pin
+  // is also where the reads are waited for
+  auto pin = [&](i32x8 (&av)[4], i32x8 (&bv)[4]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[i], bv[j], acc[i][j], 0, 0, 2 * S,
-                                                                       int(ta[i]), 2 * S, int(tb[j]));
-    };
-    kstep(std::integral_constant<int, 0>{});
-    kstep(std::integral_constant<int, 1>{});
+    for (int b = 0; b < 4; ++b) asm volatile("" : "+v"(av[b]), "+v"(bv[b]));
+  };
+  auto mm = [&](const i32x8 (&av)[4], const i32x8 (&bv)[4], const uint32_t (&ta)[4], const uint32_t (&tb)[4],
+                auto sc) __attribute__((always_inline)) {
+    constexpr int S = decltype(sc)::value;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[i], bv[j], acc[i][j], 0, 0, 2 * S,
+                                                                     int(ta[i]), 2 * S, int(tb[j]));
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+
+  // Software pipeline: the LDS reads of the next K step are in flight while the
+  // current step's 16 MFMAs run. Stage st + 2 is DMA'd into stage st's buffers
+  // once every wave has read them (the barrier after the step-1 reads).
+  uint32_t ra[4], rb[4], ta[4], tb[4];
+  i32x8 r0a[4], r0b[4], r1a[4], r1b[4];
+  fetch(0, a0, b0, ra, rb);
+  wait_vm();
+  block_sync();
+  unpack(ra, rb, ta, tb);
+  if (nst > 1) fetch(1, a1, b0 + kStageB, ra, rb);
+  rd(a0, b0, S0{}, r0a, r0b);
+  pin(r0a, r0b);
+
+  auto stage = [&](int st, unsigned char* ca, unsigned char* cb, const unsigned char* na,
+                   const unsigned char* nb) __attribute__((always_inline)) {
+    rd(ca, cb, S1{}, r1a, r1b);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(r0a, r0b, ta, tb, S0{});
+    __builtin_amdgcn_sched_barrier(0);
+    pin(r1a, r1b);
+    uint32_t tn[4], tm[4];
+    // on the last stage the reads below fetch stale LDS data that is never used;
+    // keeping them unconditional keeps the operand registers in place
+    wait_vm();     // this wave's DMA of stage st+1 (and its scale words) landed ...
+    block_sync();  // ... for every wave, and every wave has read stage st
+    unpack(ra, rb, tn, tm);
+    if (st + 2 < nst) fetch(st + 2, ca, cb, ra, rb);
+    rd(na, nb, S0{}, r0a, r0b);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(r1a, r1b, ta, tb, S1{});
+    __builtin_amdgcn_sched_barrier(0);
+    pin(r0a, r0b);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) ta[b] = tn[b], tb[b] = tm[b];
   };
   for (int st = 0; st < nst; st += 2) {
-    stage(st, a0, b0, a1, b1);
-    if (st + 1 < nst) stage(st + 1, a1, b1, a0, b0);
+    stage(st, a0, b0, a1, b0 + kStageB);
+    if (st + 1 < nst) stage(st + 1, a1, b0 + kStageB, a0, b0);
   }
   wait_vm();  // no LDS-DMA may land after the work-group ends
 
-  // epilogue: C[n][m] -> Y[m][n]; lane column m, rows n = 8g + 4h + (0..3) per block.
-  // One m block at a time, one row pointer per block, compile-time n offsets.
-  const bool vec = (reinterpret_cast<uintptr_t>(y) & 7) == 0 && ldy % 4 == 0;
-  const int nl = n0 + wn + 4 * h;  // this lane's first n
-#pragma unroll 1
-  for (int j = 0; j < 4; ++j) {
-    const int m = m0 + wm + j * 32 + n;
-    if (m >= M) continue;
-    uint16_t* rowp = y + int64_t(m) * ldy + nl;
+  // epilogue through LDS: the 256 x 256 bf16 Y tile (row m = 512 B of n) fills
+  // the stage buffers. Lane (m = lane % 32 of block j, h = lane / 32) holds n =
+  // 8g + 4h + (0..3) of block i; 16-byte chunk q of row m sits at q ^ (m % 16), so
+  // the 8-byte writes and the 16-byte row reads are free of bank conflicts, and
+  // each row goes out as coalesced 16-byte stores.
+  block_sync();  // every wave is done with the operand buffers
+  {
+    const int xs = lane & 15;  // m % 16 (wm and 32 j are multiples of 16)
+    unsigned char* wp = lds + (wm + n) * 512 + 8 * h + wn * 2;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int off = i * 32 + 8 * g;
-        float v4[4];
+        const int cs = ((4 * i + g) ^ xs) << 4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v4[e] = acc[i][j][4 * g + e];
-        if (vec && nl + off + 3 < N) {
-          u32x2* d2 = reinterpret_cast<u32x2*>(rowp + off);
-          if (beta) {
-            const u32x2 old = *d2;
+        for (int j = 0; j < 4; ++j) {
+          const f32x16& c = acc[i][j];
+          float v[4] = {c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
+          if (beta) {  // Y += C with one rounding: add the old values in fp32 here
+            const int m = m0 + wm + 32 * j + n, nb = n0 + wn + 32 * i + 8 * g + 4 * h;
+            if (m < M) {
+              const uint16_t* p = y + int64_t(m) * ldy + nb;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v4[e] += bf2f(uint16_t(old[e >> 1] >> ((e & 1) * 16)));
+              for (int e = 0; e < 4; ++e)
+                if (nb + e < N) v[e] += bf2f(p[e]);
+            }
           }
-          *d2 = u32x2{pack_bf16x2(v4[0], v4[1]), pack_bf16x2(v4[2], v4[3])};
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (nl + off + e < N) rowp[off + e] = f2bf(beta ? v4[e] + bf2f(rowp[off + e]) : v4[e]);
+          *reinterpret_cast<u32x2*>(wp + j * 32 * 512 + cs) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         }
       }
+  }
+  block_sync();
+  const bool vec = (reinterpret_cast<uintptr_t>(y) & 15) == 0 && ldy % 8 == 0;
+  const int c = threadIdx.x & 31, nn = n0 + 8 * c;
+#pragma unroll 4
+  for (int it = 0; it < 32; ++it) {
+    const int r = it * 8 + (threadIdx.x >> 5), m = m0 + r;
+    if (m >= M) break;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + r * 512 + ((c ^ (r & 15)) << 4));
+    uint16_t* p = y + int64_t(m) * ldy + nn;
+    if (vec && nn + 7 < N) {
+      *reinterpret_cast<u32x4*>(p) = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (nn + e < N) p[e] = uint16_t(v[e >> 1] >> ((e & 1) * 16));
+    }
   }
 }
 
@@ -299,7 +359,7 @@ hipError_t launch_mxfp8_gemm(const uint8_t* wq, const uint8_t* wsf, const uint8_
   const int64_t blocks = int64_t(ntn) * ntm;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL(mxfp8_gemm, dim3(unsigned(blocks)), dim3(256), 0, s, wq, wsf, xq, xsf, y, ldy, M, N, K, beta,
-                     ntn);
+                     ntn, ntm);
   return hipGetLastError();
 }
 
