@@ -6,7 +6,8 @@ S=4352, D=128, 200 of 256 text keys valid. A step is one attention call over tha
 batch with inputs resident in HBM. `value` is the BF16 flash kernel's TFLOP/s
 (FLOP = 4*H*Sq*Skv*D, nominal Skv); the Sage INT8/FP8 path on config 3 (same shape,
 K outlier channels) is reported in the same line under "sage", end to end including
-its quantize prologue and kernel-only.
+its quantize prologue and kernel-only; the MXFP8 block-scaled GEMM of the DiT linears
+(the reference's quoted M=8192 N=12288 K=4096) under "blockscale".
 
 Prints ONE JSON line. --gpus above 1 is refused: this build runs on one GPU.
 """
@@ -84,6 +85,58 @@ def cpu_baseline(q, k, v, mask, S, H, D, budget_s: float = 12.0):
                       f"full call extrapolated {dt * S / n * 1e3:.0f} ms"}
 
 
+BS_M, BS_N, BS_K = 8192, 12288, 4096  # the reference's quoted block-scaled GEMM shape (src/kernels/blockscale.h:2)
+BS_REF_TFLOPS = 152.0                 # its MXFP8 figure there (RTX 5060 Ti, cuBLASLt)
+
+
+def _blockscale_setup(dev):
+    """MXFP8 operands of the quoted shape: W [N, K] quantized once, activations X [M, K];
+    returns the GEMM call Y[M, N] = X W^T (bf16 out)."""
+    import torch
+
+    from miroxen_amd.blockscale import QMat, QMode, gemm_blockscaled, qdata_bytes, qscale_bytes, quantize_blockscaled
+    g = torch.Generator(device=dev).manual_seed(41)
+    x = torch.randn(BS_M, BS_K, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(BS_N, BS_K, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    mk = lambda r: QMat(torch.empty(qdata_bytes(QMode.MXFP8, r, BS_K), dtype=torch.uint8, device=dev),
+                        torch.empty(qscale_bytes(QMode.MXFP8, r, BS_K), dtype=torch.uint8, device=dev))
+    X, W = mk(BS_M), mk(BS_N)
+    quantize_blockscaled(QMode.MXFP8, w, BS_K, BS_N, BS_K, W)
+    quantize_blockscaled(QMode.MXFP8, x, BS_K, BS_M, BS_K, X)
+    y = torch.empty(BS_M, BS_N, dtype=torch.bfloat16, device=dev)
+    return lambda: gemm_blockscaled(QMode.MXFP8, W, X, y, BS_N, BS_M, BS_N, BS_K)
+
+
+def blockscale_leg(dev, steps: int, warmup: int, warm_s: float) -> dict:
+    """MXFP8 block-scaled GEMM at the reference's quoted shape, and the activation
+    quantizer at the reference's bench shapes (tests/blockscale_test.cpp:139), bytes
+    counted as there: bf16 input + e4m3 output."""
+    import torch
+
+    from miroxen_amd.blockscale import QMat, QMode, qdata_bytes, qscale_bytes, quantize_blockscaled
+    run = _blockscale_setup(dev)
+    n = max(5, steps // 4)
+    ms = _time(run, n, warmup, warm_s)
+    tf = 2.0 * BS_M * BS_N * BS_K / (ms * 1e-3) / 1e12
+    quant = {}
+    for (M, K) in ((4096, 4096), (4096, 12288)):
+        x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+        qm = QMat(torch.empty(qdata_bytes(QMode.MXFP8, M, K), dtype=torch.uint8, device=dev),
+                  torch.empty(qscale_bytes(QMode.MXFP8, M, K), dtype=torch.uint8, device=dev))
+        mq = _time(lambda: quantize_blockscaled(QMode.MXFP8, x, K, M, K, qm), steps, warmup, warm_s)
+        gbs = (2.0 * M * K + M * K) / (mq * 1e-3) / 1e9
+        quant[f"{M}x{K}"] = {"us": round(mq * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
+    return {
+        "workload": f"MXFP8 GEMM Y[M,N] = X[M,K] W[N,K]^T, M={BS_M} N={BS_N} K={BS_K}, bf16 out",
+        "steps": n, "ms": round(ms, 4), "tflops": round(tf, 1),
+        "reference_published_tflops": BS_REF_TFLOPS, "reference_hardware": "RTX 5060 Ti (cuBLASLt)",
+        "dtype": "e4m3 x e4m3, UE8M0 scale per 32, fp32 accumulate",
+        "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_FP8, "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_FP8, 4), "traffic": _traffic("mxfp8_gemm")},
+        "quantize": quant,
+    }
+
+
 def _only(which: str, n: int) -> int:
     """Run one kernel n times on the bench inputs (for rocprofv3 --pmc passes)."""
     import torch
@@ -96,6 +149,12 @@ def _only(which: str, n: int) -> int:
         b = torch.empty_like(a)
         for _ in range(n):
             b.copy_(a)
+        torch.cuda.synchronize()
+        return 0
+    if which == "blockscale":
+        run = _blockscale_setup(dev)
+        for _ in range(n):
+            run()
         torch.cuda.synchronize()
         return 0
     cfg = CONFIGS[2 if which == "bf16" else 3]
@@ -140,7 +199,8 @@ def main() -> int:
                     help="minimum seconds of untimed back-to-back calls before each timed region")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--skip-large", action="store_true", help="skip configs 4 and 5 (S=12544, S=32760)")
-    ap.add_argument("--only", choices=["bf16", "sage", "prologue", "fused", "copy"],
+    ap.add_argument("--no-blockscale", action="store_true", help="skip the MXFP8 block-scaled GEMM leg")
+    ap.add_argument("--only", choices=["bf16", "sage", "prologue", "fused", "copy", "blockscale"],
                     help="profiling driver: run just this kernel --steps times (no warm-up, no JSON); "
                          "'copy' is a 256 MiB device copy for calibrating HBM byte counters")
     args = ap.parse_args()
@@ -258,6 +318,8 @@ def main() -> int:
                 "sage_tflops_kernel": round(fc / (mk * 1e-3) / 1e12, 1)}
             del qc, kc, vc, oc, wc
 
+    bs = None if args.no_blockscale else blockscale_leg(dev, args.steps, args.warmup, args.warm_seconds)
+
     traffic = _traffic("flash_bf16_config2")
     line = {
         "metric": "attention TFLOP/s + % MFMA peak at H=24,S=4352,D=128 (BF16 and Sage INT8/FP8)",
@@ -272,6 +334,7 @@ def main() -> int:
                      "frac": round(tflops / PEAK_BF16, 4), "traffic": traffic},
         "sage": sage,
         "other_configs": others,
+        "blockscale": bs,
         "timed_wall_s": round(wall, 3),
     }
     if not args.no_cpu:
