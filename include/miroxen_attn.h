@@ -155,9 +155,10 @@ int mx_flash_attn_fp8_norm_rope(const void* q, const void* k, const void* v, voi
  * scale per 32 K values, on gfx950's scaled MFMA. MX_QMODE_NVFP4 (e4m3 scales per
  * 16 values + a per-tensor scale) has no gfx950 scaled-MFMA form: qmode_supported
  * reports 0 and the caller keeps BF16, as the reference does on cards without it.
- * Scale layout: sf[r * kbp + kb] with kbp = K/32 rounded up to 4, rows padded to
- * 128 (the reference's qscale_bytes size; its cuBLASLt 128x4 interleave is not
- * reproduced: only this library reads the scales). */
+ * Scale layout: the reference's 128x4 interleave (blockscale.cu:82, decoded by
+ * tests/blockscale_test.cpp:15-17): scale (r, kb) at byte (r/128)*kbp*128 +
+ * (kb/4)*512 + (r%32)*16 + ((r%128)/32)*4 + kb%4, kbp = K/32 rounded up to 4, rows
+ * padded to 128; padding bytes hold 127 (1.0). */
 enum { MX_QMODE_BF16 = 0, MX_QMODE_MXFP8 = 1, MX_QMODE_NVFP4 = 2 };
 int mx_qmode_supported(int mode, int device, int* supported);
 size_t mx_qdata_bytes(int mode, int64_t rows, int64_t K);

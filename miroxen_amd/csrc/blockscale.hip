@@ -48,8 +48,10 @@ __global__ void __launch_bounds__(256) mxfp8_quant(const uint16_t* __restrict__ 
   const int64_t id = int64_t(blockIdx.x) * 256 + threadIdx.x;  // over rows_pad * kbp
   if (id >= rows_pad * kbp) return;
   const int64_t r = id / kbp, kb = id % kbp;
+  // the reference's 128 x 4 interleaved scale layout (blockscale.cu:82)
+  const int64_t so = (r / 128) * kbp * 128 + (kb / 4) * 512 + (r % 32) * 16 + (r % 128) / 32 * 4 + kb % 4;
   if (r >= rows || kb >= nkb) {  // padding: scale 1.0
-    sf[id] = 127;
+    sf[so] = 127;
     return;
   }
   const uint16_t* src = x + r * ldx + kb * kMxBlock;
@@ -85,7 +87,7 @@ __global__ void __launch_bounds__(256) mxfp8_quant(const uint16_t* __restrict__ 
   u32x4* dst = reinterpret_cast<u32x4*>(q + r * K + kb * kMxBlock);
   dst[0] = w[0];
   dst[1] = w[1];
-  sf[id] = uint8_t(e + 127);
+  sf[so] = uint8_t(e + 127);
 }
 
 // ---------------- GEMM ----------------
@@ -147,25 +149,24 @@ mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, cons
   const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wq + int64_t(n0) * K, uint32_t(int64_t(N - n0) * K));
   const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xq + int64_t(m0) * K, uint32_t(int64_t(M - m0) * K));
   const OpAddr oa = op_addr(K, lane, wave_u);
-  // scales: one u32 (4 K blocks = one stage) per (lane, row block); rows past the
-  // 128-padded matrix read as zeros (their data is zero too)
+  // Scales, in the reference's 128 x 4 interleaved layout: byte (r / 128) kbp 128 +
+  // (kb / 4) 512 + (r % 32) 16 + ((r % 128) / 32) 4 + kb % 4. A wave's 128 rows are one
+  // 128-row band, so lane n's four row blocks (r % 32 = n, (r % 128) / 32 = b) for the
+  // four K blocks of stage st (kb / 4 = st) are the 16 contiguous bytes at
+  // band + st 512 + 16 n: one 16-byte load per operand per stage. Bands past the
+  // 128-padded matrix read as zeros (their data is zero too).
   const int n = lane & 31, h = lane >> 5;
   const __amdgpu_buffer_rsrc_t rsw = buf_rsrc(wsf, uint32_t(pad_up(N, 128) * kbp));
   const __amdgpu_buffer_rsrc_t rsx = buf_rsrc(xsf, uint32_t(pad_up(M, 128) * kbp));
-  uint32_t sw_off[4], sx_off[4];
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    sw_off[b] = uint32_t(n0 + wn + b * 32 + n) * uint32_t(kbp);
-    sx_off[b] = uint32_t(m0 + wm + b * 32 + n) * uint32_t(kbp);
-  }
-  // raw scale words of stage st (K blocks 4 st .. 4 st + 3), loaded a stage ahead
-  // and unpacked only after the next stage's wait, so no stage waits on their latency
+  const uint32_t sw_off = uint32_t((n0 + wn) / 128) * uint32_t(kbp) * 128u + uint32_t(16 * n);
+  const uint32_t sx_off = uint32_t((m0 + wm) / 128) * uint32_t(kbp) * 128u + uint32_t(16 * n);
+  // raw scale words of stage st (word b = row block b), loaded a stage ahead and
+  // unpacked only after the next stage's wait, so no stage waits on their latency
   auto scales = [&](int st, uint32_t (&ra)[4], uint32_t (&rb)[4]) __attribute__((always_inline)) {
+    const u32x4 wa = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsw, sw_off + uint32_t(st * 512), 0, 0));
+    const u32x4 wb = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsx, sx_off + uint32_t(st * 512), 0, 0));
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      ra[b] = __builtin_amdgcn_raw_buffer_load_b32(rsw, sw_off[b] + uint32_t(st * 4), 0, 0);
-      rb[b] = __builtin_amdgcn_raw_buffer_load_b32(rsx, sx_off[b] + uint32_t(st * 4), 0, 0);
-    }
+    for (int b = 0; b < 4; ++b) ra[b] = wa[b], rb[b] = wb[b];
   };
 
   // LDS operand reads: rows row0 + n of an operand tile for K step s. In the f8

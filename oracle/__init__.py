@@ -197,13 +197,43 @@ def head_norm_rope(inp, S, in_stride, col0, H, D, norm_w=None, eps=0.0, cos=None
 
 def mxfp8_quantize(x, rows, K, ldx=0):
     """MXFP8 quantizer (reference blockscale.cu:69-108): x bf16 bits [rows, ldx] ->
-    (q uint8 [rows, K] e4m3, sf uint8 [rows, K/32] UE8M0)."""
+    (q uint8 [rows, K] e4m3, sf uint8 [rows, K/32] UE8M0, logical order; the device
+    buffer's interleaved order is mx_scale_pack / mx_scale_unpack)."""
     x = _c(x, np.uint16)
     ldx = ldx or K
     q = np.zeros((rows, K), np.uint8)
     sf = np.zeros((rows, K // 32), np.uint8)
     lib().or_mxfp8_quantize(_ptr(x), ldx, rows, K, _ptr(q), _ptr(sf))
     return q, sf
+
+
+def mx_sf_offset(r, kb, nkb_pad):
+    """Byte offset of scale (row r, K block kb) in the block-scaled scale buffer: the
+    128 x 4 interleaved tiles of the reference (quantizer src/kernels/blockscale.cu:82,
+    decoder tests/blockscale_test.cpp:15-17). Each 128-row band holds nkb_pad / 4 tiles of
+    512 bytes; inside a tile, row r % 32 owns 16 bytes, split into four 4-byte groups by
+    (r % 128) / 32, and kb % 4 picks the byte."""
+    r = np.asarray(r, np.int64); kb = np.asarray(kb, np.int64)
+    return (r // 128) * nkb_pad * 128 + (kb // 4) * 512 + (r % 32) * 16 + (r % 128) // 32 * 4 + kb % 4
+
+
+def mx_scale_pack(sf, rows, K, fill=127):
+    """Logical scales [rows, K/32] -> the interleaved buffer (pad128(rows) x pad4(K/32) bytes);
+    padding positions hold `fill`."""
+    nkb = K // 32
+    nkp = (nkb + 3) // 4 * 4
+    buf = np.full(((rows + 127) // 128 * 128) * nkp, fill, np.uint8)
+    r, kb = np.meshgrid(np.arange(rows), np.arange(nkb), indexing="ij")
+    buf[mx_sf_offset(r, kb, nkp)] = sf
+    return buf
+
+
+def mx_scale_unpack(buf, rows, K):
+    """The interleaved scale buffer -> logical scales [rows, K/32]."""
+    nkb = K // 32
+    nkp = (nkb + 3) // 4 * 4
+    r, kb = np.meshgrid(np.arange(rows), np.arange(nkb), indexing="ij")
+    return np.asarray(buf, np.uint8).reshape(-1)[mx_sf_offset(r, kb, nkp)]
 
 
 def gemm_mxfp8(wq, wsf, xq, xsf, M, N, K, threads=0):

@@ -23,8 +23,7 @@ def _quant(x, rows, K, cuda, ldx=None):
 
 
 def _sf_view(sf, rows, K):
-    kbp = (K // 32 + 3) // 4 * 4
-    return sf.cpu().numpy().reshape(-1, kbp)[:rows, : K // 32]
+    return oracle.mx_scale_unpack(sf.cpu().numpy(), rows, K)
 
 
 def test_modes(cuda):
@@ -47,10 +46,9 @@ def test_quantizer_bit_exact(cuda, rows, K, pad):
     assert np.array_equal(q.cpu().numpy()[: rows * K].reshape(rows, K), wq)
     assert np.array_equal(_sf_view(sf, rows, K), ws)
     assert np.all(q.cpu().numpy()[rows * K:] == 0), "wrote past the data"
-    # padding scale bytes hold 1.0 (127), so padded blocks contribute 0 x 1 in the GEMM
-    kbp = (K // 32 + 3) // 4 * 4
-    full = sf.cpu().numpy().reshape(-1, kbp)
-    assert np.all(full[rows:] == 127) and np.all(full[:, K // 32:] == 127)
+    # the whole buffer is the reference's interleaved layout of the scales, and padding
+    # positions hold 1.0 (127), so padded blocks contribute 0 x 1 in the GEMM
+    np.testing.assert_array_equal(sf.cpu().numpy(), oracle.mx_scale_pack(ws, rows, K))
 
 
 @pytest.mark.parametrize("M,N,K,beta", [

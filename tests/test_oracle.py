@@ -481,6 +481,26 @@ def test_mxfp8_quantizer_scale_rule_and_exact_values():
     assert np.all(err <= np.maximum(np.abs(xf) * 2.0 ** -4, scale * 2.0 ** -10) * (1 + 1e-12))
 
 
+def test_mx_scale_layout():
+    """The interleaved scale layout: a bijection onto pad128(rows) x pad4(K/32) bytes, the
+    reference quantizer's row base (blockscale.cu:82: sf + (r/128) nkb_pad 128 + (r%32) 16 +
+    ((r%128)/32) 4) plus its decoder's block term ((kb/4) 512 + kb%4, blockscale_test.cpp:16)
+    at hand-picked points, and pack / unpack inverse to each other."""
+    rows, K = 300, 32 * 10                       # nkb = 10 -> padded to 12, rows padded to 384
+    nkp = 12
+    r, kb = np.meshgrid(np.arange(384), np.arange(nkp), indexing="ij")
+    off = oracle.mx_sf_offset(r, kb, nkp).reshape(-1)
+    assert np.array_equal(np.sort(off), np.arange(384 * nkp))
+    f = lambda a, b: int(oracle.mx_sf_offset(a, b, nkp))
+    assert [f(0, 0), f(0, 1), f(0, 3), f(0, 4), f(1, 0), f(31, 0), f(32, 0), f(96, 0), f(127, 3), f(128, 0)] == \
+        [0, 1, 3, 512, 16, 496, 4, 12, 511, 128 * nkp]
+    assert f(130, 5) == 128 * nkp + 512 + 2 * 16 + 1
+    sf = np.random.default_rng(5).integers(0, 255, (rows, K // 32)).astype(np.uint8)
+    buf = oracle.mx_scale_pack(sf, rows, K)
+    assert buf.size == 384 * nkp and np.array_equal(oracle.mx_scale_unpack(buf, rows, K), sf)
+    assert np.count_nonzero(buf == 127) >= 384 * nkp - rows * (K // 32)
+
+
 def test_mxfp8_gemm_oracle_matches_numpy():
     """The GEMM oracle against a numpy float64 restatement (dequantize, matmul), and the
     identity: W = I with unit scales returns the dequantized X."""
