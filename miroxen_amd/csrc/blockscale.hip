@@ -112,14 +112,15 @@ __device__ __forceinline__ OpAddr op_addr(int64_t K, int lane, int wave) {
   return a;
 }
 
-template <bool KTAIL>
+// Lanes whose chunk lies past K read zeros (an offset past the buffer's range);
+// for a stage wholly past K every lane does, and the DMA only clears LDS.
 __device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rs, const OpAddr& a, int64_t K, int k0,
                                           unsigned char* dst, int wave) {
-  const bool past = KTAIL && uint32_t(k0) + a.chunk >= uint32_t(K);
+  const bool past = uint32_t(k0) + a.chunk >= uint32_t(K);
 #pragma unroll
   for (int jj = 0; jj < 8; ++jj) {
     const int j = 4 * jj + wave;
-    const uint32_t off = past ? 0x80000000u : a.vo[jj];  // past K: read as zeros
+    const uint32_t off = past ? 0x80000000u : a.vo[jj];
     buf2lds16(rs, off, uint32_t(k0), (MXA_LDS void*)(dst + j * 1024));
   }
 }
@@ -144,7 +145,6 @@ mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, cons
   const int wn = (wave & 1) * 128, wm = (wave >> 1) * 128;
   const int kbp = int(pad_up(K / kMxBlock, 4));
   const int nst = (K + kStage - 1) / kStage;
-  const bool ktail = K % kStage != 0;
 
   const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wq + int64_t(n0) * K, uint32_t(int64_t(N - n0) * K));
   const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xq + int64_t(m0) * K, uint32_t(int64_t(M - m0) * K));
@@ -205,13 +205,8 @@ mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, cons
   // DMA of stage st (operands and the raw scale words) into buffers (da, db)
   auto fetch = [&](int st, unsigned char* da, unsigned char* db, uint32_t (&ra)[4],
                    uint32_t (&rb)[4]) __attribute__((always_inline)) {
-    if (ktail && st + 1 == nst) {
-      dma_stage<true>(rw, oa, K, st * kStage, da, wave_u);
-      dma_stage<true>(rx, oa, K, st * kStage, db, wave_u);
-    } else {
-      dma_stage<false>(rw, oa, K, st * kStage, da, wave_u);
-      dma_stage<false>(rx, oa, K, st * kStage, db, wave_u);
-    }
+    dma_stage(rw, oa, K, st * kStage, da, wave_u);
+    dma_stage(rx, oa, K, st * kStage, db, wave_u);
     scales(st, ra, rb);
   };
   // byte 0: K block 2s + h of step s = 0, byte 2: of step s = 1 (op_sel 0 / 2)
@@ -235,14 +230,16 @@ mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, cons
 #pragma unroll
     for (int b = 0; b < 4; ++b) asm volatile("" : "+v"(av[b]), "+v"(bv[b]));
   };
+  // MFMAs [lo, hi) of a K step, in (i, j) order
   auto mm = [&](const i32x8 (&av)[4], const i32x8 (&bv)[4], const uint32_t (&ta)[4], const uint32_t (&tb)[4],
-                auto sc) __attribute__((always_inline)) {
+                auto sc, auto lo, auto hi) __attribute__((always_inline)) {
     constexpr int S = decltype(sc)::value;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[i], bv[j], acc[i][j], 0, 0, 2 * S,
+        if (4 * i + j >= decltype(lo)::value && 4 * i + j < decltype(hi)::value)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[i], bv[j], acc[i][j], 0, 0, 2 * S,
                                                                      int(ta[i]), 2 * S, int(tb[j]));
   };
   using S0 = std::integral_constant<int, 0>;
@@ -257,27 +254,45 @@ mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, cons
   wait_vm();
   block_sync();
   unpack(ra, rb, ta, tb);
-  if (nst > 1) fetch(1, a1, b0 + kStageB, ra, rb);
+  fetch(1, a1, b0 + kStageB, ra, rb);
   rd(a0, b0, S0{}, r0a, r0b);
   pin(r0a, r0b);
 
+  using C0 = std::integral_constant<int, 0>;
+  using C2 = std::integral_constant<int, 2>;
+  using C16 = std::integral_constant<int, 16>;
+  // Stage body. Step 0's MFMAs are interleaved with step 1's LDS reads; two of
+  // step 1's MFMAs are issued before the stage barrier so the matrix unit stays
+  // busy while the wave waits there; the remaining 14 are interleaved with the
+  // DMA of stage st + 2 (unconditional: a stage past K only clears LDS that is
+  // never read) and with the LDS reads of the next stage's step 0 (on the last
+  // stage they fetch stale data that is never used).
   auto stage = [&](int st, unsigned char* ca, unsigned char* cb, const unsigned char* na,
                    const unsigned char* nb) __attribute__((always_inline)) {
     rd(ca, cb, S1{}, r1a, r1b);
-    __builtin_amdgcn_sched_barrier(0);
-    mm(r0a, r0b, ta, tb, S0{});
+    mm(r0a, r0b, ta, tb, S0{}, C0{}, C16{});
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
     __builtin_amdgcn_sched_barrier(0);
     pin(r1a, r1b);
+    mm(r1a, r1b, ta, tb, S1{}, C0{}, C2{});
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t tn[4], tm[4];
-    // on the last stage the reads below fetch stale LDS data that is never used;
-    // keeping them unconditional keeps the operand registers in place
     wait_vm();     // this wave's DMA of stage st+1 (and its scale words) landed ...
     block_sync();  // ... for every wave, and every wave has read stage st
     unpack(ra, rb, tn, tm);
-    if (st + 2 < nst) fetch(st + 2, ca, cb, ra, rb);
+    fetch(st + 2, ca, cb, ra, rb);
     rd(na, nb, S0{}, r0a, r0b);
-    __builtin_amdgcn_sched_barrier(0);
-    mm(r1a, r1b, ta, tb, S1{});
+    mm(r1a, r1b, ta, tb, S1{}, C2{}, C16{});
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM: DMA, scale loads
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+    }
     __builtin_amdgcn_sched_barrier(0);
     pin(r0a, r0b);
 #pragma unroll
