@@ -1,12 +1,15 @@
 // The reference's invalid-input checks (tests/attention_test.cu:178-208) through
 // the C++ drop-in header: 11 bad parameter sets x {flash_attn, attn_reference}
-// plus a null query must each throw std::runtime_error. Validation happens on the
-// host before any launch, so this runs without a GPU.
+// plus a null query must each throw std::runtime_error; the block-scaled GEMM
+// header's sizes (the reference test's shapes, tests/blockscale_test.cpp:135-136)
+// and its MX_CHECK-style rejections. Validation happens on the host before any
+// launch, so this runs without a GPU.
 #include <cstdio>
 #include <limits>
 #include <stdexcept>
 
 #include "miroxen/attention.h"
+#include "miroxen/blockscale.h"
 #include "miroxen/head_norm_rope.h"
 
 using namespace mx;
@@ -51,11 +54,33 @@ int main() {
   } catch (const std::runtime_error&) {
     ++nr_rejected;
   }
+  // block-scaled GEMM: sizes of the reference test's shapes, then host-side rejections
+  int bs_ok = 0;
+  bs_ok += qdata_bytes(QMode::MXFP8, 300, 1024) == size_t(300) * 1024;
+  bs_ok += qscale_bytes(QMode::MXFP8, 300, 1024) == size_t(384) * 32;   // rows -> 384, K/32 = 32
+  bs_ok += qscale_bytes(QMode::MXFP8, 129, 4160) == size_t(256) * 132;  // K/32 = 130 -> 132
+  bs_ok += parse_qmode("fp8") == QMode::MXFP8 && parse_qmode("") == QMode::BF16 &&
+           std::string(qmode_name(QMode::NVFP4)) == "fp4";
+  QMat qm{b, reinterpret_cast<uint8_t*>(b), nullptr};
+  auto* hb = reinterpret_cast<__hip_bfloat16*>(b);
+  const auto throws = [](auto f) {
+    try {
+      f();
+    } catch (const std::runtime_error&) {
+      return 1;
+    }
+    return 0;
+  };
+  bs_ok += throws([&] { parse_qmode("int3"); });
+  bs_ok += throws([&] { quantize_blockscaled(QMode::MXFP8, hb, 48, 4, 48, qm, nullptr); });  // K % 32
+  bs_ok += throws([&] { quantize_blockscaled(QMode::BF16, hb, 64, 4, 64, qm, nullptr); });
+  bs_ok += throws([&] { gemm_blockscaled(nullptr, QMode::MXFP8, qm, qm, hb, 64, 4, 64, 64, 0.5f); });  // beta
+  bs_ok += throws([&] { gemm_blockscaled(nullptr, QMode::NVFP4, qm, qm, hb, 64, 4, 64, 64); });
   // the workspace query is pure host arithmetic
   AttnParams c2;
   c2.Sq = 4352; c2.Skv = 4352; c2.Hq = 24; c2.Hkv = 24; c2.D = 128;
   const size_t ws = flash_attn_fp8_workspace(c2);
-  std::printf("invalid input checks: %d rejected; head_norm_rope %d rejected; config-2 workspace %zu bytes\n",
-              rejected, nr_rejected, ws);
-  return rejected == 23 && nr_rejected == 1 && ws > 0 ? 0 : 1;
+  std::printf("invalid input checks: %d rejected; head_norm_rope %d rejected; blockscale %d/9 ok; "
+              "config-2 workspace %zu bytes\n", rejected, nr_rejected, bs_ok, ws);
+  return rejected == 23 && nr_rejected == 1 && bs_ok == 9 && ws > 0 ? 0 : 1;
 }
