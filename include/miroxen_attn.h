@@ -100,6 +100,14 @@ int mx_sage_layout_of(const mx_attn_params* p, mx_sage_layout* out);
 int mx_sage_quantize(const void* q, const void* k, const void* v, const mx_attn_params* p, void* ws,
                      void* stream);
 
+/* mx_sage_quantize with a choice of Q scale group: q_group 16 is the reference's
+ * (one Q scale per 16 tokens, attention_fp8.cu:435-438); 64 gives one Q scale per
+ * 64-token block, the grouping the config-3 workload specifies. No reference
+ * counterpart. The workspace layout is unchanged (a 64-token scale is stored in each
+ * of its four 16-token entries), so mx_sage_attend runs on it as it is. */
+int mx_sage_quantize_qgroup(const void* q, const void* k, const void* v, const mx_attn_params* p, void* ws,
+                            int q_group, void* stream);
+
 /* Main kernel only, on a workspace already filled by mx_sage_quantize. */
 int mx_sage_attend(void* o, const mx_attn_params* p, const void* ws, void* stream);
 

@@ -20,7 +20,7 @@ SYMBOLS = (
     "mx_flash_attn", "mx_flash_attn_fp8_workspace", "mx_flash_attn_fp8_supported",
     "mx_flash_attn_fp8_ok", "mx_flash_attn_fp8", "mx_attn_reference", "mx_sage_layout_of",
     "mx_sage_quantize", "mx_sage_attend", "mx_last_error", "mx_version", "mx_head_norm_rope",
-    "mx_sage_quantize_norm_rope", "mx_flash_attn_fp8_norm_rope",
+    "mx_sage_quantize_norm_rope", "mx_flash_attn_fp8_norm_rope", "mx_sage_quantize_qgroup",
     "mx_qmode_supported", "mx_qdata_bytes", "mx_qscale_bytes", "mx_quantize_blockscaled", "mx_gemm_blockscaled",
 )
 
@@ -68,6 +68,7 @@ def load():
         "mx_attn_reference": ([vp, vp, vp, vp, P, vp], ctypes.c_int),
         "mx_sage_layout_of": ([P, ctypes.POINTER(CLayout)], ctypes.c_int),
         "mx_sage_quantize": ([vp, vp, vp, P, vp, vp], ctypes.c_int),
+        "mx_sage_quantize_qgroup": ([vp, vp, vp, P, vp, ctypes.c_int, vp], ctypes.c_int),
         "mx_sage_attend": ([vp, P, vp, vp], ctypes.c_int),
         "mx_last_error": ([], ctypes.c_char_p),
         "mx_version": ([], ctypes.c_char_p),

@@ -106,11 +106,16 @@ def sage_layout(p: AttnParams) -> dict:
     return {name: int(getattr(out, name)) for name, _ in _lib.CLayout._fields_}
 
 
-def sage_quantize(q, k, v, p: AttnParams, ws, stream=None) -> None:
-    """First half of flash_attn_fp8: the Q/K/V quantize prologue into ws."""
+def sage_quantize(q, k, v, p: AttnParams, ws, stream=None, q_group: int = 16) -> None:
+    """First half of flash_attn_fp8: the Q/K/V quantize prologue into ws. q_group 16 is
+    the reference's Q scale grouping; 64 = one Q scale per 64-token block."""
     c = p.c()
-    _lib.check(_lib.load().mx_sage_quantize(_addr(q), _addr(k), _addr(v), ctypes.byref(c), _addr(ws),
-                                            _stream(stream)))
+    if q_group == 16:
+        _lib.check(_lib.load().mx_sage_quantize(_addr(q), _addr(k), _addr(v), ctypes.byref(c), _addr(ws),
+                                                _stream(stream)))
+    else:
+        _lib.check(_lib.load().mx_sage_quantize_qgroup(_addr(q), _addr(k), _addr(v), ctypes.byref(c), _addr(ws),
+                                                       int(q_group), _stream(stream)))
 
 
 def sage_attend(o, p: AttnParams, ws, stream=None) -> None:

@@ -22,7 +22,7 @@ hipError_t launch_naive_attn(const uint16_t*, const uint16_t*, const uint16_t*, 
                              hipStream_t);
 mx_sage_layout sage_layout(const mx_attn_params&);
 hipError_t launch_sage_quantize(const uint16_t*, const uint16_t*, const uint16_t*, const mx_attn_params&, char*,
-                                hipStream_t, const NormRope*);
+                                hipStream_t, const NormRope*, int q_group);
 hipError_t launch_sage_attend(uint16_t*, const mx_attn_params&, const char*, hipStream_t);
 size_t mx_qscale_size(int64_t rows, int64_t K);
 hipError_t launch_mxfp8_quant(const uint16_t*, int64_t, int64_t, int64_t, uint8_t*, uint8_t*, hipStream_t);
@@ -203,7 +203,7 @@ int mx_flash_attn_fp8(const void* q, const void* k, const void* v, void* o, cons
   if (!ws || !ok) return mx_flash_attn(q, k, v, o, p, stream);  // reference :491
   auto s = static_cast<hipStream_t>(stream);
   rc = hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                                            static_cast<const uint16_t*>(v), a, static_cast<char*>(ws), s, nullptr),
+                                            static_cast<const uint16_t*>(v), a, static_cast<char*>(ws), s, nullptr, 16),
                   "flash_attn_fp8 prologue");
   if (rc) return rc;
   return hip_status(mxa::launch_sage_attend(static_cast<uint16_t*>(o), a, static_cast<const char*>(ws), s),
@@ -220,8 +220,23 @@ int mx_sage_quantize(const void* q, const void* k, const void* v, const mx_attn_
   if (!ws) return fail(MX_E_INVALID, "sage_quantize: null workspace");
   return hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                                               static_cast<const uint16_t*>(v), a, static_cast<char*>(ws),
-                                              static_cast<hipStream_t>(stream), nullptr),
+                                              static_cast<hipStream_t>(stream), nullptr, 16),
                     "sage_quantize");
+}
+
+int mx_sage_quantize_qgroup(const void* q, const void* k, const void* v, const mx_attn_params* p, void* ws,
+                            int q_group, void* stream) {
+  if (q_group != 16 && q_group != 64) return fail(MX_E_INVALID, "sage_quantize_qgroup: q_group must be 16 or 64");
+  mx_attn_params a;
+  bool ok = false;
+  int rc = sage_args(q, k, v, q, p, ws, &a, &ok);
+  if (rc) return rc;
+  if (!ok) return fail(MX_E_UNSUPPORTED, "sage_quantize_qgroup: arguments not supported by the quantized path");
+  if (!ws) return fail(MX_E_INVALID, "sage_quantize_qgroup: null workspace");
+  return hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                              static_cast<const uint16_t*>(v), a, static_cast<char*>(ws),
+                                              static_cast<hipStream_t>(stream), nullptr, q_group),
+                    "sage_quantize_qgroup");
 }
 
 // Fused head_norm_rope + Sage prologue: the head_norm_rope rules (reference
@@ -257,7 +272,7 @@ int mx_sage_quantize_norm_rope(const void* q, const void* k, const void* v, cons
   if (rc) return rc;
   return hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                                               static_cast<const uint16_t*>(v), a, static_cast<char*>(ws),
-                                              static_cast<hipStream_t>(stream), n),
+                                              static_cast<hipStream_t>(stream), n, 16),
                     "sage_quantize_norm_rope");
 }
 
@@ -274,7 +289,7 @@ int mx_flash_attn_fp8_norm_rope(const void* q, const void* k, const void* v, voi
   if (rc) return rc;
   auto s = static_cast<hipStream_t>(stream);
   rc = hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                                            static_cast<const uint16_t*>(v), a, static_cast<char*>(ws), s, n),
+                                            static_cast<const uint16_t*>(v), a, static_cast<char*>(ws), s, n, 16),
                   "flash_attn_fp8_norm_rope prologue");
   if (rc) return rc;
   return hip_status(mxa::launch_sage_attend(static_cast<uint16_t*>(o), a, static_cast<const char*>(ws), s),

@@ -54,7 +54,9 @@ constexpr int kStatChunk = 128;  // tokens staged in LDS per step of a stats blo
 // + RoPE of head_norm_rope (nq / nk, nr128_row with rope mode NRM) and its bf16
 // rounding on the way in, so the workspace is bit-identical to head_norm_rope
 // followed by the plain prologue. NRM = -1: the plain prologue.
-template <int NRM>
+// QG: Q scale group in rows, 16 (the reference) or 64 (one scale per 64-token
+// block, written to each of its four 16-row entries so the attention kernel is unchanged).
+template <int NRM, int QG>
 __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                     const uint16_t* __restrict__ v, mx_attn_params p, int nb,
                                                     float qmult, int64_t sq_pad, float* __restrict__ part,
@@ -146,6 +148,12 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
     for (int j = 0; j < 8; ++j) am = fmaxf(am, fabsf(x[i][j]));
   }
   am = wave_max(am);
+  if constexpr (QG == 64) {  // the work-group's four waves hold the 64-row block
+    __shared__ float wmax[4];
+    if (lane == 0) wmax[wave] = am;
+    __syncthreads();
+    am = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  }
   const float inv = am > 0.f ? 127.f / am : 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -725,7 +733,7 @@ mx_sage_layout sage_layout(const mx_attn_params& p) {
 // nr: null for the plain prologue, else {Q norm/rope, K norm/rope} applied on the fly
 // (D == 128 and nr128_supported, checked by the caller).
 hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint16_t* v, const mx_attn_params& p,
-                                char* ws, hipStream_t s, const NormRope* nr) {
+                                char* ws, hipStream_t s, const NormRope* nr, int q_group) {
   const mx_sage_layout L = sage_layout(p);
   const int nb = (p.Skv + kStatTok - 1) / kStatTok;
   float* part = reinterpret_cast<float*>(ws + L.part);
@@ -738,8 +746,12 @@ hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint
   const NormRope none{};
   const NormRope nq = nr ? nr[0] : none, nk = nr ? nr[1] : none;
   const int mode = nr ? nr128_mode(nq) : -1;
-  auto stats = mode < 0 ? prep_stats_q<-1> : mode == kRopeNone ? prep_stats_q<kRopeNone>
-             : mode == kRopeInterleaved ? prep_stats_q<kRopeInterleaved> : prep_stats_q<kRopeHalf>;
+  // the Q work-groups hold four consecutive 16-row groups of one head (sq_pad is a
+  // multiple of 64), i.e. one 64-row block, for the QG = 64 variant
+  static_assert(kSqPad % 64 == 0, "Q padding must cover whole 64-row blocks");
+  auto stats = q_group == 64 ? prep_stats_q<-1, 64>
+             : mode < 0 ? prep_stats_q<-1, 16> : mode == kRopeNone ? prep_stats_q<kRopeNone, 16>
+             : mode == kRopeInterleaved ? prep_stats_q<kRopeInterleaved, 16> : prep_stats_q<kRopeHalf, 16>;
   auto kvq = mode < 0 ? prep_kv_quant<-1> : mode == kRopeNone ? prep_kv_quant<kRopeNone>
            : mode == kRopeInterleaved ? prep_kv_quant<kRopeInterleaved> : prep_kv_quant<kRopeHalf>;
   hipLaunchKernelGGL(stats, dim3(unsigned(blocks1)), dim3(256), 0, s, q, k, v, p, nb, qmult, L.sq_pad, part,

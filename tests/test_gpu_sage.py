@@ -106,6 +106,42 @@ def test_prologue_bit_exact_config3(cuda):
         assert np.array_equal(g[name], want[name]), name
 
 
+def test_q_group_64_config3(cuda):
+    """Config 3 as its workload states it: one Q scale per 64-token block (q_group=64).
+    Every quantized byte and scale against the oracle quantizer with G=64 (the 64-token
+    scale sits in each of its four 16-token entries), then the attention against the
+    emulator fed that workspace and against exact attention (cosine >= 0.995)."""
+    cfg = CONFIGS[3]
+    q, k, v, mask = make_inputs(cfg, seed=3, device=cuda)
+    S, H = cfg.S, cfg.H
+    p = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128, kv_valid=mask)
+    ws = _ws(p, cuda)
+    sage_quantize(q, k, v, p, ws, q_group=64)
+    torch.cuda.synchronize()
+    L = sage_layout(p)
+    g = _quantized(ws, p, L)
+    _, want = oracle.sage_reference(_bits(q), _bits(k), _bits(v), S, S, H, H, 128, q_group=64,
+                                    rows=np.zeros(0, np.int32))
+    want["qs"] = np.repeat(want["qs"], 4, axis=1)
+    for name in ("km", "va", "qs", "ks", "qi", "ki", "vt"):
+        assert np.array_equal(g[name], want[name]), name
+    assert np.all(g["qs"][:, 0::4] == g["qs"][:, 3::4])
+    o = torch.empty_like(q)
+    sage_attend(o, p, ws)
+    torch.cuda.synchronize()
+    rows = np.array(sorted(set(query_rows(S, H)) | set(range(0, S, S // 40))), np.int32)
+    mk = mask.cpu().numpy()
+    units = (S + 255) // 256 * H
+    emu = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128, kv_valid=mk,
+                              rows=rows, headroom=oracle.KERNEL_HEADROOM,
+                              split=(units - L["split_units"], L["split_parts"]))
+    exact = oracle.attention_f64(_bits(q), _bits(k), _bits(v), S, S, H, H, 128, kv_valid=mk, rows=rows)
+    got = _f32(o[torch.from_numpy(rows).long().to(cuda)])
+    c_emu, c_ex, rr = cosine(got, emu), cosine(got, exact), rel_rms(got, exact)
+    print(f"config3 q_group=64: cos(emu)={c_emu:.7f} cos(exact)={c_ex:.6f} relrms={rr:.4f}", flush=True)
+    assert c_emu >= 0.99999 and c_ex >= 0.995 and rr < 0.045
+
+
 def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
     p = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128, kv_valid=mask)
     ws = _ws(p, cuda)
