@@ -80,7 +80,14 @@ def cpu_baseline(q, k, v, mask, S, H, D, budget_s: float = 12.0):
     oracle.attention_f64(qb, kb, vb, S, S, H, H, D, kv_valid=mk, rows=rows, threads=threads)
     dt = time.perf_counter() - t0
     flop = 4.0 * H * n * S * D
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
     return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "host_cpus": os.cpu_count(), "cpu_model": model,
             "sample": f"{n} of {S} query rows x {H} heads, all {S} keys, {dt:.1f} s; "
                       f"full call extrapolated {dt * S / n * 1e3:.0f} ms"}
 
