@@ -8,7 +8,9 @@
 // 64-value MFMA step (selected per operand by op_sel); see the operand layout note
 // in mxfp8_gemm.
 //
-// Scale layout (this build's, not cuBLASLt's 128x4 interleave): sf[r * kbp + kb],
+// Scale layout: the reference's 128 x 4 interleave (quantizer blockscale.cu:82,
+// decoder tests/blockscale_test.cpp:15-17): scale (r, kb) at byte
+// (r / 128) kbp 128 + (kb / 4) 512 + (r % 32) 16 + ((r % 128) / 32) 4 + kb % 4,
 // kbp = K/32 rounded up to 4, rows padded to 128 (the reference's qscale_bytes size).
 // The quantizer writes 127 (= 1.0) into every padding byte, so padded K blocks and
 // rows contribute 0 (data 0 times a finite scale) instead of 0 x NaN (0xFF).
@@ -19,7 +21,10 @@
 // live in AGPRs). K advances in stages of 128 bytes DMA'd into LDS
 // (buffer_load ... lds, 1 KB per op, rows past the matrix read as zeros), double
 // buffered; LDS rows are 128 B with their 16-byte chunks XOR'd by (row >> 1) & 7, so
-// each 16-lane group of an operand read hits 16 distinct chunk slots.
+// each 16-lane group of an operand read hits 16 distinct chunk slots. A stage's
+// scales for a lane are one 16-byte load per operand (the interleave puts a 128-row
+// band's four 32-row blocks side by side). The bf16 tile leaves through LDS as
+// coalesced 16-byte row stores.
 #include <type_traits>
 
 #include "attn_common.hpp"
