@@ -26,6 +26,15 @@
  *  - or_sage_emulate: pinned by its limit: with exact (unquantized) P/V it must
  *    equal or_attention_f64 to fp32 accuracy, and by the reference gate
  *    (rel-RMS < 4 % vs exact attention, tests/attention_fp8_test.cpp:65).
+ *  - or_mxfp8_quantize: pinned by the scale rule checked against float64
+ *    ceil(log2(bmax / 448)) (independent of the frexp formulation), hand cases
+ *    (zero block, bmax / 448 a power of two, just above one), exact round trips
+ *    of e4m3 values times 2^k and the half-ulp error bound. Its scales come out
+ *    in logical [rows][K/32] order; the reference's 128 x 4 interleave is
+ *    oracle.mx_sf_offset (Python), pinned by hand-picked offsets of the
+ *    reference decoder's formula and the bijection onto the padded buffer.
+ *  - or_gemm_mxfp8: pinned by a numpy float64 dequantize-and-matmul and the
+ *    identity-weight case (W = I with unit scales returns deq(X)).
  */
 #include <math.h>
 #include <stdint.h>
