@@ -111,3 +111,33 @@ def test_reference_cases_and_gates(cuda, M, N, K):
     layout_err, elem_err, quant_err = rel(got, ydec), rel(fx, x64), rel(got, x64 @ w64.T)
     print(f"layout {layout_err:.2e} element {elem_err:.4f} gemm-vs-bf16 {quant_err:.4f}", flush=True)
     assert layout_err < 5e-3 and elem_err < 0.04 and quant_err < 0.05
+
+
+def test_gemm_full_size_sampled_rows(cuda):
+    """The reference's quoted shape (M=8192, N=12288, K=4096) through the full grid: both
+    quantized operands bit-exact against the oracle quantizer, then nine output rows
+    spread over every tile row (first, last, tile edges) against the oracle GEMM of
+    those rows of X with all of W."""
+    M, N, K = 8192, 12288, 4096
+    print(f"mxfp8 full-size M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device=cuda).manual_seed(53)
+    x = (torch.randn(M, K, device=cuda, generator=g) * 2).to(torch.bfloat16)
+    w = (torch.randn(N, K, device=cuda, generator=g) * 0.05).to(torch.bfloat16)
+    xq, xs = _quant(x, M, K, cuda)
+    wq, ws = _quant(w, N, K, cuda)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=cuda)
+    gemm_blockscaled(QMode.MXFP8, QMat(wq, ws), QMat(xq, xs), y, N, M, N, K)
+    torch.cuda.synchronize()
+    bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
+    owq, ows = oracle.mxfp8_quantize(bits(w), N, K)
+    assert np.array_equal(wq.cpu().numpy()[: N * K].reshape(N, K), owq)
+    assert np.array_equal(_sf_view(ws, N, K), ows)
+    rows = np.array([0, 1, 255, 256, 2047, 4100, 6143, 8190, 8191])
+    xb = bits(x)[rows]
+    oxq, oxs = oracle.mxfp8_quantize(xb, len(rows), K)
+    assert np.array_equal(xq.cpu().numpy()[: M * K].reshape(M, K)[rows], oxq)
+    assert np.array_equal(_sf_view(xs, M, K)[rows], oxs)
+    want = oracle.gemm_mxfp8(owq, ows, oxq, oxs, len(rows), N, K).astype(np.float64)
+    got = y.float().cpu().numpy()[rows].astype(np.float64)
+    tol = np.abs(want) * 2.0 ** -7 + np.abs(want).max() * 2.0 ** -14
+    assert np.all(np.abs(got - want) <= tol), float(np.max(np.abs(got - want) - tol))
