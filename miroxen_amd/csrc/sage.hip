@@ -49,6 +49,7 @@ __device__ __forceinline__ u32x2 quant8(const float (&x)[8], float inv) {
 }
 
 constexpr int kStatChunk = 128;  // tokens staged in LDS per step of a stats block
+constexpr int kFoldNb = 32;      // statistics partials per head up to which prep_kv_quant finalizes them
 
 // NRM >= 0: q and k are the raw projections; every row gets the per-head RMS-norm
 // + RoPE of head_norm_rope (nq / nk, nr128_row with rope mode NRM) and its bf16
@@ -163,17 +164,13 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
   if (lane == 0) qs[int64_t(h) * (sq_pad / 16) + grp] = am / 127.f * qmult;
 }
 
-// kmean = sum of the partials in ascending block order from 0.f; vamax = max.
-__global__ void __launch_bounds__(D) prep_finalize(mx_attn_params p, int nb, const float* __restrict__ part,
-                                                   float* __restrict__ km, float* __restrict__ va,
-                                                   int* __restrict__ cnt, int ncnt) {
-  const int h = blockIdx.x, d = threadIdx.x;
-  if (h == 0)  // arrival counters of the attention kernel's split units start at zero
-    for (int i = d; i < ncnt; i += D) cnt[i] = 0;
-  const float* ps = part + int64_t(h) * nb * D + d;
-  const float* pa = ps + int64_t(p.Hkv) * nb * D;
-  float s = 0.f, am = 0.f;
+// kmean / vamax of one head from the statistics partials: the sum in ascending
+// block order from 0.f, the max (prep_finalize's arithmetic, shared so the fused
+// path is bit-identical).
+__device__ __forceinline__ void finalize_channel(const float* ps, const float* pa, int nb, float& s, float& am) {
   constexpr int B = 16;
+  s = 0.f;
+  am = 0.f;
   for (int b0 = 0; b0 < nb; b0 += B) {
     float xs[B], xa[B];
 #pragma unroll
@@ -188,6 +185,18 @@ __global__ void __launch_bounds__(D) prep_finalize(mx_attn_params p, int nb, con
         am = fmaxf(am, xa[j]);
       }
   }
+}
+
+// kmean = sum of the partials in ascending block order from 0.f; vamax = max.
+__global__ void __launch_bounds__(D) prep_finalize(mx_attn_params p, int nb, const float* __restrict__ part,
+                                                   float* __restrict__ km, float* __restrict__ va,
+                                                   int* __restrict__ cnt, int ncnt) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  if (h == 0)  // arrival counters of the attention kernel's split units start at zero
+    for (int i = d; i < ncnt; i += D) cnt[i] = 0;
+  const float* ps = part + int64_t(h) * nb * D + d;
+  float s, am;
+  finalize_channel(ps, ps + int64_t(p.Hkv) * nb * D, nb, s, am);
   km[h * D + d] = s;
   va[h * D + d] = am;
 }
@@ -204,21 +213,47 @@ __device__ __forceinline__ uint32_t e4m3x2_sat(float a, float b) {
 // Per (64-key tile, head): K - mean -> INT8 (one scale per tile) and V -> e4m3
 // transposed to [H][D][skv_pad] in natural key order. Thread tid owns channel
 // chunk tid%16 (8 channels) of rows tid/16 + 16*i, i = 0..3.
+// fold_nb > 0: prep_finalize is folded in (short sequences, few partials): every
+// work-group sums its head's fold_nb partials itself, work-groups of tile 0 store
+// the head's km / va, and work-group (0, 0) zeroes the attention kernel's split
+// counters. fold_nb == 0: km / va come from prep_finalize.
 template <int NRM>
 __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                                                     mx_attn_params p, int64_t skv_pad,
-                                                     const float* __restrict__ km, const float* __restrict__ va,
-                                                     int8_t* __restrict__ ki, float* __restrict__ ks,
-                                                     uint8_t* __restrict__ vt, NormRope nk) {
+                                                     mx_attn_params p, int64_t skv_pad, float* __restrict__ km,
+                                                     float* __restrict__ va, int8_t* __restrict__ ki,
+                                                     float* __restrict__ ks, uint8_t* __restrict__ vt, NormRope nk,
+                                                     int fold_nb, const float* __restrict__ part,
+                                                     int* __restrict__ cnt, int ncnt) {
   __shared__ __align__(16) uint8_t tile[D][kKvPad + 16];
   __shared__ float red[4];
+  __shared__ float kms[D], vas[D];
   const int h = blockIdx.y, k0 = blockIdx.x * kKvPad, tid = threadIdx.x;
   const int c = (tid & 15) * 8, r0 = tid >> 4;
+  const float* kmh = km + h * D;
+  const float* vah = va + h * D;
+  if (fold_nb > 0) {
+    if (tid < D) {
+      const float* ps = part + int64_t(h) * fold_nb * D + tid;
+      float sm, am;
+      finalize_channel(ps, ps + int64_t(p.Hkv) * fold_nb * D, fold_nb, sm, am);
+      kms[tid] = sm;
+      vas[tid] = am;
+      if (blockIdx.x == 0) {
+        km[h * D + tid] = sm;
+        va[h * D + tid] = am;
+      }
+    }
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+      for (int i = tid; i < ncnt; i += 256) cnt[i] = 0;
+    __syncthreads();
+    kmh = kms;
+    vah = vas;
+  }
   float mean[8], vsc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    mean[j] = km[h * D + c + j];
-    const float a = va[h * D + c + j];
+    mean[j] = kmh[c + j];
+    const float a = vah[c + j];
     vsc[j] = a > 0.f ? 448.f / a : 0.f;
   }
   u32x4 kraw[4], vraw[4];
@@ -756,11 +791,17 @@ hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint
            : mode == kRopeInterleaved ? prep_kv_quant<kRopeInterleaved> : prep_kv_quant<kRopeHalf>;
   hipLaunchKernelGGL(stats, dim3(unsigned(blocks1)), dim3(256), 0, s, q, k, v, p, nb, qmult, L.sq_pad, part,
                      reinterpret_cast<int8_t*>(ws + L.qi), reinterpret_cast<float*>(ws + L.qs), nq, nk);
-  hipLaunchKernelGGL(prep_finalize, dim3(p.Hkv), dim3(D), 0, s, p, nb, (const float*)part, km, va,
+  // up to kFoldNb statistics partials per head (Skv <= 8192) the K/V quantizer sums
+  // them itself (each work-group re-reads its head's partials from L2); beyond, that
+  // re-reading would outweigh the separate prep_finalize launch
+  const int fold = nb <= kFoldNb ? nb : 0;
+  if (!fold)
+    hipLaunchKernelGGL(prep_finalize, dim3(p.Hkv), dim3(D), 0, s, p, nb, (const float*)part, km, va,
+                       reinterpret_cast<int*>(ws + L.cnt), L.split_units);
+  hipLaunchKernelGGL(kvq, dim3(unsigned(L.skv_pad / kKvPad), p.Hkv), dim3(256), 0, s, k, v, p, L.skv_pad, km, va,
+                     reinterpret_cast<int8_t*>(ws + L.ki), reinterpret_cast<float*>(ws + L.ks),
+                     reinterpret_cast<uint8_t*>(ws + L.vt), nk, fold, (const float*)part,
                      reinterpret_cast<int*>(ws + L.cnt), L.split_units);
-  hipLaunchKernelGGL(kvq, dim3(unsigned(L.skv_pad / kKvPad), p.Hkv), dim3(256), 0, s, k, v, p, L.skv_pad,
-                     (const float*)km, (const float*)va, reinterpret_cast<int8_t*>(ws + L.ki),
-                     reinterpret_cast<float*>(ws + L.ks), reinterpret_cast<uint8_t*>(ws + L.vt), nk);
   return hipGetLastError();
 }
 
