@@ -142,6 +142,25 @@ def test_q_group_64_config3(cuda):
     assert c_emu >= 0.99999 and c_ex >= 0.995 and rr < 0.045
 
 
+@pytest.mark.parametrize("Sq,Skv,Hq,Hkv,pad", [(300, 300, 4, 4, 0), (130, 517, 4, 2, 8), (64, 64, 2, 2, 0)])
+def test_q_group_64_prologue_bit_exact(cuda, Sq, Skv, Hq, Hkv, pad):
+    """Q per 64 tokens on small shapes: a partial last 64-row block (rows past Sq count
+    as zeros), GQA, padded strides; every workspace region against the oracle with G = 64."""
+    D = 128
+    print(f"q_group=64 prologue {Sq}x{Skv} H={Hq}/{Hkv} pad={pad}", flush=True)
+    q, k, v, qs, ks = _bias_inputs(Sq, Skv, Hq, Hkv, D, pad, 2.0, cuda, Sq * 13 + Skv)
+    p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=D, q_stride=qs, kv_stride=ks, o_stride=qs)
+    ws = _ws(p, cuda)
+    sage_quantize(q, k, v, p, ws, q_group=64)
+    torch.cuda.synchronize()
+    g = _quantized(ws, p, sage_layout(p))
+    _, want = oracle.sage_reference(_bits(q), _bits(k), _bits(v), Sq, Skv, Hq, Hkv, D, q_stride=qs, kv_stride=ks,
+                                    q_group=64, rows=np.zeros(0, np.int32))
+    want["qs"] = np.repeat(want["qs"], 4, axis=1)
+    for name in ("km", "va", "qs", "ks", "qi", "ki", "vt"):
+        assert np.array_equal(g[name], want[name]), name
+
+
 def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
     p = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128, kv_valid=mask)
     ws = _ws(p, cuda)
