@@ -54,6 +54,7 @@ def test_quantizer_bit_exact(cuda, rows, K, pad):
 @pytest.mark.parametrize("M,N,K,beta", [
     (256, 256, 128, 0.0), (300, 200, 96, 0.0), (77, 513, 4096, 1.0), (1024, 768, 3072, 0.0), (33, 31, 160, 1.0),
     (512, 512, 256, 1.0),  # beta = 1 on the aligned (16-byte store) path: ldy = N + 8
+    (1, 1, 32, 0.0), (1, 300, 64, 1.0),  # the smallest shapes: one row, one column, one K block
 ])
 def test_gemm_matches_oracle(cuda, M, N, K, beta):
     print(f"mxfp8 gemm M={M} N={N} K={K} beta={beta}", flush=True)
