@@ -114,6 +114,34 @@ def _blockscale_setup(dev):
     return lambda: gemm_blockscaled(QMode.MXFP8, W, X, y, BS_N, BS_M, BS_N, BS_K)
 
 
+def blockscale_cpu_baseline(budget_s: float = 8.0) -> dict:
+    """The oracle's MXFP8 GEMM (C restatement: dequantize, double accumulation, OpenMP over
+    output rows) timed on a bounded sample of X rows at the quoted shape, all of W."""
+    import numpy as np
+
+    import oracle
+    threads = min(os.cpu_count() or 1, 16)
+    rng = np.random.default_rng(41)
+    wq = rng.integers(0, 0x7E, (BS_N, BS_K), dtype=np.uint8)
+    ws = np.full((BS_N, BS_K // 32), 120, np.uint8)
+    rows = 8
+    xq = rng.integers(0, 0x7E, (rows, BS_K), dtype=np.uint8)
+    xs = np.full((rows, BS_K // 32), 127, np.uint8)
+    t0 = time.perf_counter()
+    oracle.gemm_mxfp8(wq, ws, xq, xs, rows, BS_N, BS_K, threads=threads)
+    dt = max(time.perf_counter() - t0, 1e-3)
+    rows = int(min(512, max(8, rows * budget_s / dt)))
+    xq = rng.integers(0, 0x7E, (rows, BS_K), dtype=np.uint8)
+    xs = np.full((rows, BS_K // 32), 127, np.uint8)
+    t0 = time.perf_counter()
+    oracle.gemm_mxfp8(wq, ws, xq, xs, rows, BS_N, BS_K, threads=threads)
+    dt = time.perf_counter() - t0
+    flop = 2.0 * rows * BS_N * BS_K
+    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of {BS_M} rows of X against all of W ({BS_N} x {BS_K}), {dt:.1f} s; "
+                      f"full GEMM extrapolated {dt * BS_M / rows:.0f} s"}
+
+
 def blockscale_leg(dev, steps: int, warmup: int, warm_s: float) -> dict:
     """MXFP8 block-scaled GEMM at the reference's quoted shape, and the activation
     quantizer at the reference's bench shapes (tests/blockscale_test.cpp:139), bytes
@@ -338,6 +366,8 @@ def main() -> int:
             del qc, kc, vc, oc, wc
 
     bs = None if args.no_blockscale else blockscale_leg(dev, args.steps, args.warmup, args.warm_seconds)
+    if bs is not None and not args.no_cpu:
+        bs["cpu_baseline"] = blockscale_cpu_baseline()
 
     traffic = _traffic("flash_bf16_config2")
     line = {
