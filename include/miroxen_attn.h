@@ -84,15 +84,20 @@ int mx_attn_reference(const void* q, const void* k, const void* v, void* o, cons
 /* Byte offsets of the workspace regions (256-byte aligned each) and padded lengths.
  *   qi [Hq][sq_pad][D] int8, ki [Hkv][skv_pad][D] int8, vt [Hkv][D][skv_pad] e4m3,
  *   qs [Hq][sq_pad/16] f32, ks [Hkv][skv_pad/64] f32, km [Hkv][D] f32 (K mean),
- *   va [Hkv][D] f32 (V abs-max), part: kv_stats partials,
+ *   va [Hkv][D] f32 (V abs-max), part: kv_stats partials, tab (after part): per key
+ *   tile its 64 liveness bits and K scale, for the attention kernel,
  *   split: partial outputs of the key-range-split work-groups that balance the
- *   attention grid's last round over the device's CUs (split_units units in
- *   split_parts parts each; 0 when the grid divides evenly), cnt: one int32
- *   arrival counter per split unit (zeroed by the prologue, left zero by the kernel). */
+ *   attention grid's last round over an MI355X's 256 CUs (split_units units of
+ *   split_qt query rows in split_parts parts each; 0 when the grid divides evenly),
+ *   cnt: one int32 arrival counter per split unit (zeroed by the prologue, left zero
+ *   by the kernel). Every field is a pure function of the parameters (no device
+ *   query), as the reference's layout (src/kernels/attention_fp8.cu:471-473). */
 typedef struct mx_sage_layout {
   int64_t sq_pad, skv_pad;
   size_t qi, ki, vt, qs, ks, km, va, part, split, cnt, total;
   int split_units, split_parts;
+  int split_qt; /* query rows per grid unit of the attention kernel (128 or 256) */
+  size_t tab;   /* [Hkv][skv_pad/64 + 1] 16-byte tile entries: liveness bits, K scale */
 } mx_sage_layout;
 int mx_sage_layout_of(const mx_attn_params* p, mx_sage_layout* out);
 

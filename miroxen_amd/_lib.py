@@ -44,7 +44,8 @@ class CNormRope(ctypes.Structure):
 class CLayout(ctypes.Structure):
     _fields_ = [("sq_pad", ctypes.c_int64), ("skv_pad", ctypes.c_int64)] + [
         (n, ctypes.c_size_t) for n in ("qi", "ki", "vt", "qs", "ks", "km", "va", "part", "split", "cnt", "total")] + [
-        ("split_units", ctypes.c_int), ("split_parts", ctypes.c_int)]
+        ("split_units", ctypes.c_int), ("split_parts", ctypes.c_int), ("split_qt", ctypes.c_int),
+        ("tab", ctypes.c_size_t)]
 
 
 _lib = None

@@ -18,6 +18,7 @@ using f32x2 = __attribute__((ext_vector_type(2))) float;
 using i32x16 = __attribute__((ext_vector_type(16))) int;
 using i32x8 = __attribute__((ext_vector_type(8))) int;
 using i32x4 = __attribute__((ext_vector_type(4))) int;
+using i32x32 = __attribute__((ext_vector_type(32))) int;
 using u32x4 = __attribute__((ext_vector_type(4))) unsigned;
 using u32x2 = __attribute__((ext_vector_type(2))) unsigned;
 

@@ -12,6 +12,7 @@
 
 #include "attn_common.hpp"
 #include "norm_rope.hpp"
+#include "sage_tile.inc"
 
 
 namespace mxa {
@@ -223,7 +224,7 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
                                                      float* __restrict__ va, int8_t* __restrict__ ki,
                                                      float* __restrict__ ks, uint8_t* __restrict__ vt, NormRope nk,
                                                      int fold_nb, const float* __restrict__ part,
-                                                     int* __restrict__ cnt, int ncnt) {
+                                                     int* __restrict__ cnt, int ncnt, u32x4* __restrict__ tab) {
   __shared__ __align__(16) uint8_t tile[D][kKvPad + 16];
   __shared__ float red[4];
   __shared__ float kms[D], vas[D];
@@ -305,6 +306,16 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
   for (int i = 0; i < 4; ++i)
     *reinterpret_cast<u32x2*>(ki + (int64_t(h) * skv_pad + k0 + r0 + 16 * i) * D + c) = quant8(x[i], inv);
   if (tid == 0) ks[int64_t(h) * (skv_pad / kKvPad) + blockIdx.x] = am / 127.f * 1.f;
+  // tile table of the attention kernel: liveness bits of the tile's 64 keys (mask and
+  // tail) and its K scale
+  if (tid < 64) {
+    const int64_t key = k0 + tid;
+    const bool live = key < p.Skv && (!p.kv_valid || p.kv_valid[key]);
+    const uint64_t bits = __ballot(live);
+    if (tid == 0)
+      tab[int64_t(h) * (skv_pad / kKvPad + 1) + blockIdx.x] =
+          u32x4{uint32_t(bits), uint32_t(bits >> 32), __float_as_uint(am / 127.f * 1.f), 0u};
+  }
   // V^T rows: channel d, 64 keys = 4 x 16 bytes
   for (int i = tid; i < D * (kKvPad / 16); i += 256) {
     const int d = i / (kKvPad / 16), u = i % (kKvPad / 16);
@@ -347,13 +358,14 @@ constexpr int KT = 64;
 constexpr int KTILEB = KT * D;        // 8 KB int8 K tile
 constexpr int VTILEB = D * KT;        // 8 KB fp8 V^T tile
 constexpr int STAGEB = KTILEB + VTILEB;
-// Split partial of one work-group (see sage_plan): acc as [8 waves][16 float4]
-// [64 lanes], then m and l as [8 waves][64 lanes][2].
-constexpr int kSplitAcc = 8 * 16 * 64 * 4, kSplitFloats = kSplitAcc + 8 * 64 * 2;
+// Split partial of one work-group of NW waves (see sage_plan): acc as [NW waves]
+// [16 float4][64 lanes], then m and l as [NW waves][64 lanes][2].
+constexpr int split_acc(int nw) { return nw * 16 * 64 * 4; }
+constexpr int split_floats(int nw) { return split_acc(nw) + nw * 64 * 2; }
 constexpr int kMaxParts = 4;  // bounds the merge's reads (parts x 132 KB per unit)
 struct SageSplit {
   int full, parts;  // work-groups [0, full) run whole units; the rest run one of `parts` key ranges
-  float* part;      // partials, kSplitFloats per split work-group
+  float* part;      // partials, split_floats(NW) per split work-group
   int* cnt;         // arrival counter per split unit
 };
 constexpr float kSageHeadroom = 2.f;
@@ -469,6 +481,7 @@ __device__ __forceinline__ void sage_load_k(const SageAddr& a, int tk, unsigned 
 // End of a work-group: a split part publishes (acc, m, l) and returns unless it is
 // the last of its unit to arrive, which merges every part; then O = acc * vamax[d] /
 // (448 l) -> bf16 for this lane's query row.
+template <int NW>
 __device__ __forceinline__ void sage_finish(f32x16 (&acc)[4], float m, float l, int part, int su, const SageSplit& sp,
                                             int wave, int lane, int row, const mx_attn_params& p,
                                             const float* __restrict__ va, int kvh, int head,
@@ -480,6 +493,7 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[4], float m, float l, 
     // XCDs' non-coherent L2s for these lines only; a device-scope fence would write
     // back and invalidate a whole L2 and with it every other work-group's K/V.
     constexpr int kSc1 = 16;  // cache policy: device scope
+    constexpr int kSplitAcc = split_acc(NW), kSplitFloats = split_floats(NW);
     const uint32_t unit_bytes = uint32_t(sp.parts) * kSplitFloats * 4;
     const __amdgpu_buffer_rsrc_t rp = buf_rsrc(sp.part + int64_t(su) * sp.parts * kSplitFloats, unit_bytes);
     const uint32_t lacc = uint32_t(wave * 16 * 64 + lane) * 16u;          // + j * 1024 for float4 j
@@ -688,42 +702,263 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   }
 
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
-  sage_finish(acc, m, l, part, su, sp, wave, lane, row, p, va, kvh, head, o);
+  sage_finish<NW>(acc, m, l, part, su, sp, wave, lane, row, p, va, kvh, head, o);
+}
+
+// ---------------- software-pipelined main kernel ----------------
+//
+// Same work-group shape, unit/split mapping, LDS tile layouts and arithmetic as
+// sage_attn_d128, but each wave overlaps its own matrix and vector work: in the
+// iteration of tile t it runs the online softmax of S(t) while it issues the score
+// MFMAs of S(t+1) and the P(t-1) V(t-1) MFMAs, and it ends with the row max of S(t+1)
+// and the LDS operands of iteration t+1 already in registers. The whole tile loop is
+// one inline-assembly statement (sage_tile.inc; gen_sage_tile.py states the schedule,
+// the register map and the hazards it respects); this function sets up its registers
+// and LDS and finishes the output.
+//
+// LDS: K tiles in a ring of four 8 KB slots (tile j in slot j % 4), V^T tiles in
+// another, and a table of 16 bytes per tile (liveness bits of its 64 keys, K scale).
+// K(j) is read in iterations j-2 and j-1, V(j) in iterations j and j+1. Iteration t
+// DMAs K(t+4) and V(t+2) into the slots of K(t) and V(t-2), last read in iteration
+// t-1 (before the barrier at the top of iteration t); its DMA ops are waited for at
+// the top of iteration t+2, before the first read of their tiles.
+//
+// Accumulator frames: before block A of iteration t the output accumulator holds
+// P(..t-2) V in the frame of m(t-1); A and B add P(t-1) V(t-1), and the rescale by
+// alpha(t) = 2^(m(t-1) - m(t)) follows B. The row sum l is rescaled before B, which
+// adds this tile's sum (per wave half: the halves are combined once, at the end).
+constexpr int kPipeMaxTiles = 512;  // tile table entries (8 KB of LDS): Skv <= 32768
+constexpr int kPipeWaves = 4;       // 128 queries per work-group, two work-groups per CU
+
+__global__ void __launch_bounds__(256, 2)
+sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, const uint8_t* __restrict__ vt_g,
+               const float* __restrict__ qs, const u32x4* __restrict__ tab_g, const float* __restrict__ va,
+               uint16_t* __restrict__ o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad, SageSplit sp) {
+  constexpr int NW = kPipeWaves, QT = NW * 32;
+  __shared__ __align__(16) unsigned char kring[4 * KTILEB];
+  __shared__ __align__(16) unsigned char vring[4 * VTILEB];
+  __shared__ __align__(16) u32x4 table[kPipeMaxTiles + 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 31, h = lane >> 5;
+  const int ntq = (p.Sq + QT - 1) / QT;
+  const int nkt = (p.Skv + KT - 1) / KT;
+  int L, tb = 0, nt = nkt, su = 0, part = -1;
+  if (int(blockIdx.x) < sp.full) {
+    L = xcd_remap(blockIdx.x, sp.full);
+  } else {  // split units, part-major (see sage_attn_d128)
+    const int j = int(blockIdx.x) - sp.full, nsu = (int(gridDim.x) - sp.full) / sp.parts;
+    part = j / nsu;
+    su = j - part * nsu;
+    L = sp.full + su;
+    tb = int(int64_t(part) * nkt / sp.parts);
+    nt = int(int64_t(part + 1) * nkt / sp.parts);
+  }
+  const int head = L / ntq, qtile = L % ntq;
+  const int kvh = head / (p.Hq / p.Hkv);
+  const int row = qtile * QT + wave * 32 + n;  // < sq_pad
+  const int last = nt - 1;
+
+  // K/V^T DMA of a tile: 8 K ops and 8 V^T ops of 1 KB, two of each per wave. K op j
+  // (j = 2w, 2w+1) fills rows (j & 1) * 32 + lane / 2 of d-chunk w (16-byte halves
+  // swapped on rows 32..63); V^T op j fills channel rows 16 j + lane / 4. A tile past the
+  // last is replaced by the last.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int kr = lane >> 1, vr = lane >> 2;
+  const uint32_t lk0 = uint32_t(kr * D + ((lane & 1) << 4));
+  const uint32_t lk1 = uint32_t((32 + kr) * D + (((lane & 1) ^ 1) << 4)) - 4096u;  // soffset adds 4096
+  const uint32_t lv = uint32_t(vr) * uint32_t(skv_pad) + uint32_t(((lane & 3) ^ ((vr >> 2) & 3)) << 4);
+  const uint32_t ksoff = uint32_t(wave_u * 32), vsoff = uint32_t(2 * wave_u * 16) * uint32_t(skv_pad);
+  const uint32_t vstep = uint32_t(16) * uint32_t(skv_pad);
+  const __amdgpu_buffer_rsrc_t rk_r = buf_rsrc(ki + int64_t(kvh) * skv_pad * D, uint32_t(skv_pad * D));
+  const __amdgpu_buffer_rsrc_t rv_r = buf_rsrc(vt_g + int64_t(kvh) * D * skv_pad, uint32_t(skv_pad * D));
+  auto dma_k = [&](int tile, int slot) __attribute__((always_inline)) {
+    const uint32_t so = ksoff + uint32_t((tile < last ? tile : last) * (KT * D));
+    unsigned char* d = kring + (slot & 3) * KTILEB + 2 * wave_u * 1024;
+    buf2lds16(rk_r, lk0, so, (MXA_LDS void*)d);
+    buf2lds16(rk_r, lk1, so + 4096u, (MXA_LDS void*)(d + 1024));
+  };
+  auto dma_v = [&](int tile, int slot) __attribute__((always_inline)) {
+    const uint32_t so = vsoff + uint32_t((tile < last ? tile : last) * KT);
+    unsigned char* d = vring + (slot & 3) * VTILEB + 2 * wave_u * 1024;
+    buf2lds16(rv_r, lv, so, (MXA_LDS void*)d);
+    buf2lds16(rv_r, lv, so + vstep, (MXA_LDS void*)(d + 1024));
+  };
+  dma_k(tb, tb);
+  dma_k(tb + 1, tb + 1);
+  dma_k(tb + 2, tb + 2);
+  dma_k(tb + 3, tb + 3);
+  dma_v(tb, tb);
+  dma_v(tb + 1, tb + 1);
+  dma_v(tb, tb + 3);  // stands in for V(tb - 1) (read with P(tb - 1) = 0): finite bytes
+
+  i32x4 qf[4];
+  {
+    const int8_t* src = qi + (int64_t(head) * sq_pad + row) * D + h * 16;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) qf[cc] = *reinterpret_cast<const i32x4*>(src + cc * 32);
+  }
+  const float qscale = qs[int64_t(head) * (sq_pad / 16) + row / 16];
+  // tile table (liveness bits, K scale; written by the prologue's prep_kv_quant): one
+  // coalesced 16-byte load per lane; the entry past the last tile is read by the last
+  // iteration (its result is unused)
+  {
+    const u32x4* tg = tab_g + int64_t(kvh) * (skv_pad / KT + 1);
+    u32x4 e[(kPipeMaxTiles + NW * 64 - 1) / (NW * 64)];
+#pragma unroll
+    for (int j = 0; j < int(sizeof(e) / sizeof(e[0])); ++j) {
+      const int i = int(threadIdx.x) + j * NW * 64;
+      if (i < nkt) e[j] = tg[i];
+    }
+#pragma unroll
+    for (int j = 0; j < int(sizeof(e) / sizeof(e[0])); ++j) {
+      const int i = int(threadIdx.x) + j * NW * 64;
+      if (i < nkt) table[i] = e[j];
+    }
+    if (threadIdx.x == 0) table[nkt] = u32x4{~0u, ~0u, 0u, 0u};
+  }
+  wait_vm_n<0>();
+  __syncthreads();  // K(tb..tb+3), V(tb), V(tb+1) and the tile table are visible
+
+  // per-lane LDS read bases
+  const int krow = kperm(0, n);
+  const uint32_t kbase = uint32_t(krow * 32 + ((h ^ ((krow >> 5) & 1)) << 4));
+  const int vsw = (n >> 2) & 3;
+  const uint32_t vbase0 = uint32_t(n * 64 + (((2 * h) ^ vsw) << 4));
+  const uint32_t vbase1 = uint32_t(n * 64 + (((2 * h + 1) ^ vsw) << 4));
+  const uint32_t kring_l = uint32_t(uintptr_t((MXA_LDS unsigned char*)kring));
+  const uint32_t vring_l = uint32_t(uintptr_t((MXA_LDS unsigned char*)vring));
+  const uint32_t table_l = uint32_t(uintptr_t((MXA_LDS u32x4*)table));
+
+  // S(tb) (masked) and its row max; the first iteration's operand registers
+  i32x16 s0, s1;
+  {
+    const unsigned char* kd = kring + (tb & 3) * KTILEB + kbase;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const i32x4 a0 = *reinterpret_cast<const i32x4*>(kd + cc * 2048);
+      const i32x4 a1 = *reinterpret_cast<const i32x4*>(kd + cc * 2048 + 512);
+      s0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, qf[cc], cc == 0 ? kScoreBias16 : s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, qf[cc], cc == 0 ? kScoreBias16 : s1, 0, 0, 0);
+    }
+  }
+  const u32x4 tab0 = table[tb];
+  const uint32_t lw0 = h ? tab0[1] : tab0[0];
+  int im;
+  {
+    int mx = kDead;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (!((lw0 >> i) & 1u)) s0[i] = kDead;
+      if (!((lw0 >> (16 + i)) & 1u)) s1[i] = kDead;
+      mx = max(mx, max(s0[i], s1[i]));
+    }
+    im = max(mx, other_half_i(mx));
+  }
+  const i32x32 stb = __builtin_shufflevector(s0, s1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17,
+                                             18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31);
+  i32x32 sbuf0 = stb, sbuf1 = stb;  // S(tb) goes to buffer tb % 2 (the other one is overwritten)
+  i32x8 kt;                          // K(tb+1) chunk 0 of both key blocks
+  i32x16 vtr;                        // V(tb) channel blocks 0, 1 (stands in for V(tb - 1))
+  {
+    const unsigned char* kd = kring + ((tb + 1) & 3) * KTILEB + kbase;
+    const i32x4 k0 = *reinterpret_cast<const i32x4*>(kd), k1 = *reinterpret_cast<const i32x4*>(kd + 512);
+    kt = __builtin_shufflevector(k0, k1, 0, 1, 2, 3, 4, 5, 6, 7);
+    const unsigned char* vd = vring + (tb & 3) * VTILEB;
+    const i32x4 a = *reinterpret_cast<const i32x4*>(vd + vbase0), b = *reinterpret_cast<const i32x4*>(vd + vbase1);
+    const i32x4 c = *reinterpret_cast<const i32x4*>(vd + vbase0 + 2048);
+    const i32x4 d = *reinterpret_cast<const i32x4*>(vd + vbase1 + 2048);
+    vtr = __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7),
+                                  __builtin_shufflevector(c, d, 0, 1, 2, 3, 4, 5, 6, 7), 0, 1, 2, 3, 4, 5, 6, 7, 8, 9,
+                                  10, 11, 12, 13, 14, 15);
+  }
+  const i32x16 q16 = __builtin_shufflevector(__builtin_shufflevector(qf[0], qf[1], 0, 1, 2, 3, 4, 5, 6, 7),
+                                             __builtin_shufflevector(qf[2], qf[3], 0, 1, 2, 3, 4, 5, 6, 7), 0, 1,
+                                             2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+  const i32x16 bias = kScoreBias16;
+  // table entries by tile parity (v[228:230] / v[232:234]), v231 = the second K op's
+  // per-lane offset; the entry of tile tb goes to both parities
+  const i32x4 tabi = __builtin_bit_cast(i32x4, tab0);
+  i32x8 tabs = __builtin_shufflevector(tabi, tabi, 0, 1, 2, 3, 4, 5, 6, 7);
+  tabs[3] = int(lk1);
+  i32x16 pbuf = {};  // P buffers; P(tb - 1) = 0
+  f32x16 acc0 = {}, acc1 = {}, acc2 = {}, acc3 = {};
+  // running max, exponent offset and scale of tile tb (the loop computes them for the
+  // next tile at the end of each iteration): m = tmax unless every key is dead
+  const float sc = fmaxf(qscale * __uint_as_float(tab0[2]), 1e-30f), c2 = 12582912.f * sc;
+  float m = __builtin_fmaf(__int_as_float(im), sc, -c2);  // -inf when every key of tile tb is dead
+  float nm = (kLog2_448 - kSageHeadroom - fmaxf(m, -3.0e38f)) - c2;
+  float l = 0.f, alpha0 = 1.f, alpha1 = 1.f;
+  uint64_t pend0 = 0, pend1 = 0;  // the accumulators need no rescale at tile tb
+  int t = tb;
+  int s_0, s_1, s_2, m0save;  // scalar scratch of the loop (M0 is saved and restored)
+  const uint32_t kdm0 = kring_l + uint32_t(2 * wave_u * 1024), vdm0 = vring_l + uint32_t(2 * wave_u * 1024);
+  const uint32_t tab1 = table_l + 16u;
+  const uint64_t hmask = 0xffffffff00000000ull;
+  float sc_v = sc;
+  const uint32_t kb_l = kring_l + kbase, vb0_l = vring_l + vbase0, vb1_l = vring_l + vbase1;
+  // the buffer resources as plain words (gfx9 dword3: 32-bit data, no swizzle)
+  auto rsrc_words = [](const void* base, uint32_t bytes) __attribute__((always_inline)) {
+    const uint64_t a = uint64_t(uintptr_t(base));
+    return i32x4{int(uint32_t(a)), int(uint32_t(a >> 32) & 0xffffu), int(bytes), 0x00020000};
+  };
+  const i32x4 rk = rsrc_words(ki + int64_t(kvh) * skv_pad * D, uint32_t(skv_pad * D));
+  const i32x4 rv = rsrc_words(vt_g + int64_t(kvh) * D * skv_pad, uint32_t(skv_pad * D));
+  asm volatile(SAGE_TILE_LOOP
+               : "+{v[0:15]}"(acc0), "+{v[16:31]}"(acc1), "+{v[32:47]}"(acc2), "+{v[48:63]}"(acc3),
+                 "+{v[64:95]}"(sbuf0), "+{v[96:127]}"(sbuf1), "+{v[128:143]}"(pbuf), "+{v[144:151]}"(kt),
+                 "+{v[152:167]}"(vtr), "+{v219}"(m), "+{v220}"(l), "+{v226}"(im), "+{v[228:235]}"(tabs),
+                 "+{v222}"(sc_v), "+{v223}"(nm), "+{v239}"(alpha0), "+{v225}"(alpha1), [t] "+s"(t),
+                 [s0] "=&s"(s_0), [s1] "=&s"(s_1), [s2] "=&s"(s_2), [pend0] "+s"(pend0), [pend1] "+s"(pend1),
+                 [m0save] "=&s"(m0save)
+               : "{v[168:183]}"(q16), "{v[184:199]}"(bias), "{v216}"(kb_l), "{v217}"(vb0_l), "{v218}"(vb1_l),
+                 "{v221}"(qscale), "{v236}"(lk0), "{v237}"(lv), [nt] "s"(nt), [last] "s"(last), [ksoff] "s"(ksoff),
+                 [vsoff] "s"(vsoff), [vstep] "s"(vstep), [kdm0] "s"(kdm0), [vdm0] "s"(vdm0), [tab1] "s"(tab1),
+                 [rk] "s"(rk), [rv] "s"(rv), [hmask] "s"(hmask), [kdead] "s"(kDead)
+               : "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", "v211",
+                 "v212", "v213", "v214", "v215", "v224", "v227", "v238", "vcc", "scc", "memory");
+  wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
+  f32x16 acc[4] = {acc0, acc1, acc2, acc3};
+  l += other_half(l);  // the wave halves summed different keys of the same rows
+  sage_finish<NW>(acc, m, l, part, su, sp, wave, lane, row, p, va, kvh, head, o);
 }
 
 }  // namespace
 
 // Workspace carve-up (kept in one place for the host code and the kernels).
-// Work split of the attention grid. One work-group (8 waves, 256 queries of one
-// head) fills a CU, so a grid of U units on C CUs runs in ceil(U / C) rounds and
-// the last one leaves CUs idle when C does not divide U (config 2: 408 units on 256
-// CUs, 1.59 rounds of work in 2). The last U % C units are therefore split by key
-// range into S parts, S chosen to minimise the tail's length ceil(r S / C) / S in
-// units (config 2: S = 3, tail 2/3 of a unit instead of 1); each part writes its
-// unnormalised output and the last part to finish merges them.
+// Two main kernels: sage_attn_pipe (4 waves, 128 queries per work-group, two
+// work-groups per CU; key tiles up to kPipeMaxTiles) and sage_attn_d128 (8 waves, 256
+// queries, one work-group per CU; any length). The choice depends on Skv only.
+struct SageShape {
+  bool pipe;
+  int qt, nw, per_cu;
+};
+SageShape sage_shape(const mx_attn_params& p) {
+  const bool pipe = (p.Skv + KT - 1) / KT <= kPipeMaxTiles;
+  return pipe ? SageShape{true, kPipeWaves * 32, kPipeWaves, 2} : SageShape{false, 256, 8, 1};
+}
+
+// Work split of the attention grid. A grid of U units (head, query tile) on C
+// work-group slots runs in ceil(U / C) rounds, and the last one leaves slots idle when
+// C does not divide U (config 2 on the 8-wave kernel: 408 units on 256 CUs, 1.59
+// rounds of work in 2). The last U % C units are therefore split by key range into S
+// parts, S chosen to minimise the tail's length ceil(r S / C) / S in units; each part
+// writes its unnormalised output and the last part to finish merges them.
+// C is the nominal slot count of an MI355X (256 CUs times the work-groups per CU), not
+// the current device's: the workspace size and layout are a pure function of the
+// shape, and on a device with another CU count the split stays correct (only its
+// balance changes).
+constexpr int kNominalCUs = 256;
 struct SagePlan {
   int full;   // work-groups that run a whole unit (a multiple of C, or all units)
   int units;  // split units (the last `units` units of the grid)
   int parts;  // parts per split unit
 };
-int device_cus() {
-  static int cus[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (!cus[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
 SagePlan sage_plan(const mx_attn_params& p) {
-  constexpr int QT = 256;
-  const int64_t ntq = (int64_t(p.Sq) + QT - 1) / QT, U64 = ntq * p.Hq;
+  const SageShape sh = sage_shape(p);
+  const int64_t ntq = (int64_t(p.Sq) + sh.qt - 1) / sh.qt, U64 = ntq * p.Hq;
   const int nt = (p.Skv + kKvPad - 1) / kKvPad;
-  const int C = device_cus();
+  const int C = kNominalCUs * sh.per_cu;
   SagePlan pl{int(U64 < 0x7fffffff ? U64 : 0x7fffffff), 0, 1};
-  if (C <= 0 || U64 >= 0x7fffffff) return pl;
+  if (U64 >= 0x7fffffff) return pl;
   const int U = int(U64), r = U % C;
   if (r == 0) return pl;
   double best = 1.0;
@@ -740,6 +975,7 @@ mx_sage_layout sage_layout(const mx_attn_params& p) {
   const SagePlan pl = sage_plan(p);
   L.split_units = pl.units;
   L.split_parts = pl.parts;
+  L.split_qt = sage_shape(p).qt;
   L.sq_pad = (int64_t(p.Sq) + kSqPad - 1) / kSqPad * kSqPad;
   L.skv_pad = (int64_t(p.Skv) + kKvPad - 1) / kKvPad * kKvPad;
   const int64_t nb = (int64_t(p.Skv) + kStatTok - 1) / kStatTok;
@@ -757,7 +993,8 @@ mx_sage_layout sage_layout(const mx_attn_params& p) {
   L.km = take(sizeof(float) * p.Hkv * p.D);
   L.va = take(sizeof(float) * p.Hkv * p.D);
   L.part = take(sizeof(float) * 2 * p.Hkv * nb * p.D);
-  L.split = take(sizeof(float) * kSplitFloats * size_t(pl.units) * pl.parts);
+  L.tab = take(16 * size_t(p.Hkv) * size_t(L.skv_pad / kKvPad + 1));
+  L.split = take(sizeof(float) * split_floats(sage_shape(p).nw) * size_t(pl.units) * pl.parts);
   L.cnt = take(sizeof(int) * size_t(pl.units));
   L.total = off;
   return L;
@@ -801,26 +1038,32 @@ hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint
   hipLaunchKernelGGL(kvq, dim3(unsigned(L.skv_pad / kKvPad), p.Hkv), dim3(256), 0, s, k, v, p, L.skv_pad, km, va,
                      reinterpret_cast<int8_t*>(ws + L.ki), reinterpret_cast<float*>(ws + L.ks),
                      reinterpret_cast<uint8_t*>(ws + L.vt), nk, fold, (const float*)part,
-                     reinterpret_cast<int*>(ws + L.cnt), L.split_units);
+                     reinterpret_cast<int*>(ws + L.cnt), L.split_units, reinterpret_cast<u32x4*>(ws + L.tab));
   return hipGetLastError();
 }
 
 hipError_t launch_sage_attend(uint16_t* o, const mx_attn_params& p, const char* ws, hipStream_t s) {
-  constexpr int QT = 256;
-  static_assert(kSqPad % QT == 0, "Q padding must cover whole query tiles");
+  static_assert(kSqPad % 256 == 0 && kSqPad % (kPipeWaves * 32) == 0, "Q padding must cover whole query tiles");
   const mx_sage_layout L = sage_layout(p);
-  const int ntq = (p.Sq + QT - 1) / QT;
+  const SageShape sh = sage_shape(p);
+  const int ntq = (p.Sq + sh.qt - 1) / sh.qt;
   const int64_t units = int64_t(ntq) * p.Hq;
   if (units > 0x7fffffff) return hipErrorInvalidValue;
   const SageSplit sp{int(units) - L.split_units, L.split_parts,
                      reinterpret_cast<float*>(const_cast<char*>(ws) + L.split),
                      reinterpret_cast<int*>(const_cast<char*>(ws) + L.cnt)};
   const int64_t blocks = int64_t(sp.full) + int64_t(L.split_units) * L.split_parts;
-  hipLaunchKernelGGL((sage_attn_d128<MXA_SAGE_NS>), dim3(unsigned(blocks)), dim3(512), 0, s,
-                     reinterpret_cast<const int8_t*>(ws + L.qi), reinterpret_cast<const int8_t*>(ws + L.ki),
-                     reinterpret_cast<const uint8_t*>(ws + L.vt), reinterpret_cast<const float*>(ws + L.qs),
-                     reinterpret_cast<const float*>(ws + L.ks), reinterpret_cast<const float*>(ws + L.va), o, p,
-                     L.sq_pad, L.skv_pad, sp);
+  const auto qi = reinterpret_cast<const int8_t*>(ws + L.qi);
+  const auto ki = reinterpret_cast<const int8_t*>(ws + L.ki);
+  const auto vt = reinterpret_cast<const uint8_t*>(ws + L.vt);
+  const auto qs = reinterpret_cast<const float*>(ws + L.qs);
+  const auto va = reinterpret_cast<const float*>(ws + L.va);
+  if (sh.pipe)
+    hipLaunchKernelGGL(sage_attn_pipe, dim3(unsigned(blocks)), dim3(sh.nw * 64), 0, s, qi, ki, vt, qs,
+                       reinterpret_cast<const u32x4*>(ws + L.tab), va, o, p, L.sq_pad, L.skv_pad, sp);
+  else
+    hipLaunchKernelGGL(sage_attn_d128<MXA_SAGE_NS>, dim3(unsigned(blocks)), dim3(sh.nw * 64), 0, s, qi, ki, vt, qs,
+                       reinterpret_cast<const float*>(ws + L.ks), va, o, p, L.sq_pad, L.skv_pad, sp);
   return hipGetLastError();
 }
 

@@ -56,7 +56,7 @@ def lib():
         L.or_v_quant.argtypes = [_p, _i, _i, _i, _i64, _i64, _p, _p]
         L.or_sage_emulate.restype = None
         L.or_sage_emulate.argtypes = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64,
-                                      _p, _p, _i, _p, _i, _f, _i, _i]
+                                      _p, _p, _i, _p, _i, _f, _i, _i, _i]
         L.or_head_norm_rope.restype = None
         L.or_head_norm_rope.argtypes = [_p, _i64, _i64, _i64, _i, _i, _p, _f, _p, _p, _i, _i, _p]
         L.or_mxfp8_quantize.restype = None
@@ -142,10 +142,11 @@ KERNEL_HEADROOM = 2.0
 
 def sage_emulate(qi, ki, vt, qs, ks, vamax, Sq, Skv, Hq, Hkv, D, kv_valid=None, rows=None, threads=0,
                  headroom=0.0, split=None):
-    """split = (split_full, split_parts): units (head, 256-query tile) at or past
-    split_full are evaluated as split_parts key ranges and merged (the kernel's grid
-    balancing); None = sequential over all keys, as the reference."""
-    full, parts = split if split else (0, 1)
+    """split = (split_full, split_parts[, split_qt]): units (head, split_qt-query tile,
+    256 by default) at or past split_full are evaluated as split_parts key ranges and
+    merged (the kernel's grid balancing); None = sequential over all keys, as the
+    reference."""
+    full, parts, qt = (tuple(split) + (256,))[:3] if split else (0, 1, 256)
     if parts > 8:
         raise ValueError("at most 8 split parts")
     qi = _c(qi, np.int8); ki = _c(ki, np.int8); vt = _c(vt, np.uint8)
@@ -156,7 +157,7 @@ def sage_emulate(qi, ki, vt, qs, ks, vamax, Sq, Skv, Hq, Hkv, D, kv_valid=None, 
     out = np.zeros((len(rows), Hq, D), np.float32)
     lib().or_sage_emulate(_ptr(qi), _ptr(ki), _ptr(vt), _ptr(qs), _ptr(ks), _ptr(vamax), Sq, Skv,
                           Hq, Hkv, D, sq_pad, skv_pad, _ptr(mask), _ptr(rows), len(rows),
-                          _ptr(out), threads, float(headroom), int(full), int(parts))
+                          _ptr(out), threads, float(headroom), int(full), int(parts), int(qt))
     return out
 
 

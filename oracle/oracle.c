@@ -316,17 +316,20 @@ static void or_sage_range(const int8_t* qr, float qscale, const int8_t* ki, cons
   *l_io = l;
 }
 
-/* split_full / split_parts: the build's key-range split of the attention grid
- * (units = (head, 256-query tile), unit index head * ceil(Sq/256) + row/256). Units
+/* split_full / split_parts / split_qt: the build's key-range split of the attention
+ * grid (units = (head, split_qt-query tile), unit index head * ceil(Sq/split_qt) +
+ * row/split_qt). Units
  * at or past split_full run as split_parts ranges of key tiles, [j*nt/P, (j+1)*nt/P),
  * each with its own m, l, acc, merged as M = max m_j, w_j = 2^(m_j - M),
  * l = sum l_j w_j, acc = sum acc_j w_j in part order. split_parts <= 1: no split. */
 void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, const float* qs,
                      const float* ks, const float* vamax, int Sq, int Skv, int Hq, int Hkv, int D,
                      int64_t sq_pad, int64_t skv_pad, const uint8_t* kv_valid, const int* rows,
-                     int n_rows, float* out, int threads, float headroom, int split_full, int split_parts) {
+                     int n_rows, float* out, int threads, float headroom, int split_full, int split_parts,
+                     int split_qt) {
   const int group = Hq / Hkv;
-  const int ntq = (Sq + 255) / 256;
+  const int qt = split_qt > 0 ? split_qt : 256;
+  const int ntq = (Sq + qt - 1) / qt;
   float lut[256];
   for (int c = 0; c < 256; ++c) lut[c] = or_e4m3_to_f32((uint8_t)c);
 #ifdef _OPENMP
@@ -339,7 +342,7 @@ void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, cons
     const float qscale = qs[(int64_t)head * (sq_pad / 16) + row / 16];
     const float* ksh = ks + (int64_t)kvh * (skv_pad / 64);
     const int ntiles = (int)((Skv + 63) / 64);
-    const int unit = head * ntq + row / 256;
+    const int unit = head * ntq + row / qt;
     const int parts = split_parts > 1 && unit >= split_full ? split_parts : 1;
     float* acc = (float*)calloc(D, sizeof(float));
     float* pa = (float*)calloc((size_t)parts * D, sizeof(float));

@@ -87,10 +87,13 @@ def test_workspace_and_layout():
         assert L[name] % 256 == 0
     assert L["qi"] == 0 and L["ki"] == 24 * 4352 * 128 and L["vt"] == 2 * 24 * 4352 * 128
     assert flash_attn_fp8_workspace(p) == L["total"]
-    # config 2: ~40 MB, plus ~132 KB per split work-group when the device's CU count
-    # does not divide the 408-unit grid (none without a device)
-    assert L["total"] < 45e6 + 135e3 * L["split_units"] * L["split_parts"]
-    assert L["cnt"] - L["split"] >= 4 * 33792 * L["split_units"] * L["split_parts"]
+    # config 2: ~40 MB, plus one fp32 partial (acc, m, l per lane) per split work-group;
+    # the layout is a pure function of the shape (no device here): the pipelined kernel's
+    # 128-query units, 816 on 512 work-group slots, the last 304 in three key ranges
+    nw = L["split_qt"] // 32
+    assert L["split_qt"] == 128 and L["split_units"] == 304 and L["split_parts"] == 3
+    assert L["total"] < 45e6 + 4 * (nw * 4224) * L["split_units"] * L["split_parts"]
+    assert L["cnt"] - L["split"] >= 4 * (nw * 4224) * L["split_units"] * L["split_parts"]
     p2 = AttnParams(Sq=1000, Skv=77, Hq=4, Hkv=2, D=128)
     L2 = sage_layout(p2)
     assert L2["sq_pad"] == 1024 and L2["skv_pad"] == 128
@@ -124,3 +127,15 @@ def test_head_norm_rope_rejects(bad):
     with pytest.raises(RuntimeError):
         head_norm_rope(256, a["S"], a["in_stride"], a["col0"], a["H"], a["D"], None, 1e-6, a["cos"], a["sin"],
                        a["rot"], a["mode"], 512, stream=0)
+
+
+def test_sage_tile_loop_is_generated():
+    """The committed inline-assembly tile loop (sage_tile.inc) is the generator's
+    output; the generator also asserts its hazard distances while emitting it."""
+    import importlib.util
+    src = os.path.join(ROOT, "miroxen_amd", "csrc", "gen_sage_tile.py")
+    spec = importlib.util.spec_from_file_location("gen_sage_tile", src)
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    with open(os.path.join(ROOT, "miroxen_amd", "csrc", "sage_tile.inc")) as f:
+        assert f.read() == gen.generate()

@@ -131,10 +131,10 @@ def test_q_group_64_config3(cuda):
     torch.cuda.synchronize()
     rows = np.array(sorted(set(query_rows(S, H)) | set(range(0, S, S // 40))), np.int32)
     mk = mask.cpu().numpy()
-    units = (S + 255) // 256 * H
+    units = (S + L["split_qt"] - 1) // L["split_qt"] * H
     emu = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128, kv_valid=mk,
                               rows=rows, headroom=oracle.KERNEL_HEADROOM,
-                              split=(units - L["split_units"], L["split_parts"]))
+                              split=(units - L["split_units"], L["split_parts"], L["split_qt"]))
     exact = oracle.attention_f64(_bits(q), _bits(k), _bits(v), S, S, H, H, 128, kv_valid=mk, rows=rows)
     got = _f32(o[torch.from_numpy(rows).long().to(cuda)])
     c_emu, c_ex, rr = cosine(got, emu), cosine(got, exact), rel_rms(got, exact)
@@ -173,10 +173,10 @@ def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
     mk = None if mask is None else mask.cpu().numpy()
     # the kernel balances its grid by splitting the last round's units by key range;
     # the emulator follows the same plan
-    units = (S + 255) // 256 * H
+    units = (S + L["split_qt"] - 1) // L["split_qt"] * H
     emu = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128,
                               kv_valid=mk, rows=rows, headroom=oracle.KERNEL_HEADROOM,
-                              split=(units - L["split_units"], L["split_parts"]))
+                              split=(units - L["split_units"], L["split_parts"], L["split_qt"]))
     ref_rule = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128,
                                    kv_valid=mk, rows=rows, headroom=0.0)
     exact = oracle.attention_f64(_bits(q), _bits(k), _bits(v), S, S, H, H, 128, kv_valid=mk, rows=rows)
@@ -283,7 +283,8 @@ def test_split_units_dead_parts_and_repeat(cuda):
     p = AttnParams(Sq=Sq, Skv=Skv, Hq=H, Hkv=H, D=128, kv_valid=mask)
     L = sage_layout(p)
     print(f"split units {L['split_units']} parts {L['split_parts']}", flush=True)
-    assert L["split_units"] == 8 and L["split_parts"] >= 4  # 8 units on a 256-CU device
+    # fewer units than work-group slots: every unit is split, into the most parts
+    assert L["split_units"] == (Sq + L["split_qt"] - 1) // L["split_qt"] * H and L["split_parts"] == 4
     ws = _ws(p, cuda)
     outs = []
     for _ in range(3):
