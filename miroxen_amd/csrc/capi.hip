@@ -95,16 +95,19 @@ bool device_is_gfx950(int device) {
   return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
 }
 
-// Reference fp8_ok(), src/kernels/attention_fp8.cu:451-459, for this build's
-// kernel: D == 128 only (D == 64 falls back to flash_attn), positive scale (the
-// integer row max assumes a positive score scale), and the device is gfx950.
+// Reference fp8_ok(), src/kernels/attention_fp8.cu:451-459: D == 64 or 128, no causal
+// mask, aligned operands; for this build's kernels also a positive scale (the integer
+// row max assumes a positive score scale), a quantized K/V head that 32-bit buffer
+// offsets can address (skv_pad * D < 2^32), and a gfx950 device.
 int fp8_ok(const void* q, const void* k, const void* v, const void* o, const mx_attn_params& p, bool* ok) {
   *ok = false;
-  if (p.causal || p.D != 128 || p.Sq <= 0 || p.Skv <= 0 || p.Hkv <= 0 || p.Hq <= 0 || p.Hq % p.Hkv) return MX_OK;
+  if (p.causal || (p.D != 128 && p.D != 64) || p.Sq <= 0 || p.Skv <= 0 || p.Hkv <= 0 || p.Hq <= 0 || p.Hq % p.Hkv) return MX_OK;
   if (p.q_stride % 8 || p.kv_stride % 8 || p.o_stride % 2 || !aligned(q, 16) || !aligned(k, 16) ||
       !aligned(v, 16) || !aligned(o, 4))
     return MX_OK;
   if (!(p.scale > 0.f) || p.Hq > 65535 || (p.kv_valid && p.Skv > kMaxMaskedSkv)) return MX_OK;
+  const int64_t skv_pad = (int64_t(p.Skv) + mxa::kKvPad - 1) / mxa::kKvPad * mxa::kKvPad;
+  if (skv_pad * p.D >= (int64_t(1) << 32)) return MX_OK;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_status(e, "flash_attn_fp8_ok");
@@ -125,7 +128,7 @@ extern "C" {
 
 const char* mx_last_error(void) { return g_err; }
 
-const char* mx_version(void) { return "miroxen_amd gfx950 bf16:pp8x32q-k64 sage:w8x32q-k64-int8fp8"; }
+const char* mx_version(void) { return "miroxen_amd gfx950 bf16:pp8x32q-k64 sage:pipe4x32q-k64-d128,w8x32q-k64-d64-int8fp8"; }
 
 int mx_flash_attn(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p, void* stream) {
   mx_attn_params a;
@@ -244,6 +247,7 @@ int mx_sage_quantize_qgroup(const void* q, const void* k, const void* v, const m
 static int norm_rope_args(const mx_qk_norm_rope* nr, const mx_attn_params& a, const char* who,
                           mxa::NormRope out[2]) {
   if (!nr) return fail(MX_E_INVALID, "%s: null norm/rope block", who);
+  if (a.D != 128) return fail(MX_E_UNSUPPORTED, "%s: the fused norm/rope prologue is built for D = 128", who);
   const int rot = nr->rot, mode = nr->mode;
   if (!(rot >= 0 && rot <= a.D && rot % 2 == 0)) return fail(MX_E_INVALID, "%s: D=%d rot=%d", who, a.D, rot);
   if (!(mode == MX_ROPE_NONE || mode == MX_ROPE_INTERLEAVED || mode == MX_ROPE_HALF))

@@ -19,8 +19,6 @@ namespace mxa {
 
 namespace {
 
-constexpr int D = 128;
-
 // ---------------- prologue ----------------
 //
 // Three launches (the reference uses a memset and four kernels, :433-446):
@@ -58,7 +56,8 @@ constexpr int kFoldNb = 32;      // statistics partials per head up to which pre
 // followed by the plain prologue. NRM = -1: the plain prologue.
 // QG: Q scale group in rows, 16 (the reference) or 64 (one scale per 64-token
 // block, written to each of its four 16-row entries so the attention kernel is unchanged).
-template <int NRM, int QG>
+// D: head dimension, 64 or 128 (the fused norm/rope variants: 128 only).
+template <int D, int NRM, int QG>
 __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                     const uint16_t* __restrict__ v, mx_attn_params p, int nb,
                                                     float qmult, int64_t sq_pad, float* __restrict__ part,
@@ -66,6 +65,8 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
                                                     NormRope nk) {
   __shared__ __align__(16) uint16_t kt[kStatChunk * D];
   __shared__ __align__(16) uint16_t vt_[kStatChunk * D];
+  static_assert(D == 64 || D == 128, "head dimension 64 or 128");
+  static_assert(NRM < 0 || D == 128, "the fused norm/rope prologue is built for D = 128");
   const int tid = threadIdx.x, nstat = p.Hkv * nb;
   if (int(blockIdx.x) < nstat) {
     // ---- K sum / V abs-max over tokens [b*256, min(b*256+256, Skv)) of head h ----
@@ -113,7 +114,7 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
       if (tid < D) {
 #pragma unroll 16
         for (int r = 0; r < rows; ++r) sum += bf2f(kt[r * D + tid]);  // sequential, token order
-      } else {
+      } else if (tid < 2 * D) {
         const int d = tid - D;
 #pragma unroll 16
         for (int r = 0; r < rows; ++r) am = fmaxf(am, fabsf(bf2f(vt_[r * D + d])));
@@ -121,27 +122,28 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
       __syncthreads();
     }
     if (tid < D) part[(int64_t(h) * nb + b) * D + tid] = sum / float(p.Skv);
-    else part[int64_t(p.Hkv) * nb * D + (int64_t(h) * nb + b) * D + (tid - D)] = am;
+    else if (tid < 2 * D) part[int64_t(p.Hkv) * nb * D + (int64_t(h) * nb + b) * D + (tid - D)] = am;
     return;
   }
-  // ---- Q: one 16-row group per wave; lane owns 4 chunks of 8 channels ----
+  // ---- Q: one 16-row group per wave; lane owns D / 32 chunks of 8 channels ----
   const int wave = tid >> 6, lane = tid & 63;
   const int64_t gid = (int64_t(blockIdx.x) - nstat) * 4 + wave;  // group index over (head, group)
   const int ng = int(sq_pad / 16);
   if (gid >= int64_t(p.Hq) * ng) return;
   const int h = int(gid / ng), grp = int(gid % ng);
-  float x[4][8], am = 0.f;
-  u32x4 raw[4];
+  constexpr int NCH = D / 32, CPR = D / 8;  // chunks per lane, chunks per row
+  float x[NCH][8], am = 0.f;
+  u32x4 raw[NCH];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ci = lane + i * 64, r = ci >> 4, c = (ci & 15) * 8;
+  for (int i = 0; i < NCH; ++i) {
+    const int ci = lane + i * 64, r = ci / CPR, c = (ci % CPR) * 8;
     const int64_t row = int64_t(grp) * 16 + r;
     raw[i] = u32x4{0, 0, 0, 0};
     if (row < p.Sq) raw[i] = *reinterpret_cast<const u32x4*>(q + row * p.q_stride + int64_t(h) * D + c);
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = int64_t(grp) * 16 + ((lane + i * 64) >> 4);
+  for (int i = 0; i < NCH; ++i) {
+    const int64_t row = int64_t(grp) * 16 + (lane + i * 64) / CPR;
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[i][j] = bf2f(uint16_t(raw[i][j >> 1] >> ((j & 1) * 16)));
     // row r of the group on lanes 16(r&3) .. +15: the 16-lane layout of nr128_row
@@ -158,8 +160,8 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
   }
   const float inv = am > 0.f ? 127.f / am : 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ci = lane + i * 64, r = ci >> 4, c = (ci & 15) * 8;
+  for (int i = 0; i < NCH; ++i) {
+    const int ci = lane + i * 64, r = ci / CPR, c = (ci % CPR) * 8;
     *reinterpret_cast<u32x2*>(qi + (int64_t(h) * sq_pad + int64_t(grp) * 16 + r) * D + c) = quant8(x[i], inv);
   }
   if (lane == 0) qs[int64_t(h) * (sq_pad / 16) + grp] = am / 127.f * qmult;
@@ -168,6 +170,7 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
 // kmean / vamax of one head from the statistics partials: the sum in ascending
 // block order from 0.f, the max (prep_finalize's arithmetic, shared so the fused
 // path is bit-identical).
+template <int D>
 __device__ __forceinline__ void finalize_channel(const float* ps, const float* pa, int nb, float& s, float& am) {
   constexpr int B = 16;
   s = 0.f;
@@ -189,6 +192,7 @@ __device__ __forceinline__ void finalize_channel(const float* ps, const float* p
 }
 
 // kmean = sum of the partials in ascending block order from 0.f; vamax = max.
+template <int D>
 __global__ void __launch_bounds__(D) prep_finalize(mx_attn_params p, int nb, const float* __restrict__ part,
                                                    float* __restrict__ km, float* __restrict__ va,
                                                    int* __restrict__ cnt, int ncnt) {
@@ -197,7 +201,7 @@ __global__ void __launch_bounds__(D) prep_finalize(mx_attn_params p, int nb, con
     for (int i = d; i < ncnt; i += D) cnt[i] = 0;
   const float* ps = part + int64_t(h) * nb * D + d;
   float s, am;
-  finalize_channel(ps, ps + int64_t(p.Hkv) * nb * D, nb, s, am);
+  finalize_channel<D>(ps, ps + int64_t(p.Hkv) * nb * D, nb, s, am);
   km[h * D + d] = s;
   va[h * D + d] = am;
 }
@@ -213,12 +217,12 @@ __device__ __forceinline__ uint32_t e4m3x2_sat(float a, float b) {
 
 // Per (64-key tile, head): K - mean -> INT8 (one scale per tile) and V -> e4m3
 // transposed to [H][D][skv_pad] in natural key order. Thread tid owns channel
-// chunk tid%16 (8 channels) of rows tid/16 + 16*i, i = 0..3.
+// chunk tid % (D/8) (8 channels) of rows tid / (D/8) + (2048/D) i, i < D/32.
 // fold_nb > 0: prep_finalize is folded in (short sequences, few partials): every
 // work-group sums its head's fold_nb partials itself, work-groups of tile 0 store
 // the head's km / va, and work-group (0, 0) zeroes the attention kernel's split
 // counters. fold_nb == 0: km / va come from prep_finalize.
-template <int NRM>
+template <int D, int NRM>
 __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                      mx_attn_params p, int64_t skv_pad, float* __restrict__ km,
                                                      float* __restrict__ va, int8_t* __restrict__ ki,
@@ -228,15 +232,18 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
   __shared__ __align__(16) uint8_t tile[D][kKvPad + 16];
   __shared__ float red[4];
   __shared__ float kms[D], vas[D];
+  static_assert(D == 64 || D == 128, "head dimension 64 or 128");
+  static_assert(NRM < 0 || D == 128, "the fused norm/rope prologue is built for D = 128");
+  constexpr int CPR = D / 8, RPP = 256 / CPR, NI = kKvPad / RPP;  // chunks per row, rows per pass, passes
   const int h = blockIdx.y, k0 = blockIdx.x * kKvPad, tid = threadIdx.x;
-  const int c = (tid & 15) * 8, r0 = tid >> 4;
+  const int c = (tid % CPR) * 8, r0 = tid / CPR;
   const float* kmh = km + h * D;
   const float* vah = va + h * D;
   if (fold_nb > 0) {
     if (tid < D) {
       const float* ps = part + int64_t(h) * fold_nb * D + tid;
       float sm, am;
-      finalize_channel(ps, ps + int64_t(p.Hkv) * fold_nb * D, fold_nb, sm, am);
+      finalize_channel<D>(ps, ps + int64_t(p.Hkv) * fold_nb * D, fold_nb, sm, am);
       kms[tid] = sm;
       vas[tid] = am;
       if (blockIdx.x == 0) {
@@ -257,10 +264,10 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
     const float a = vah[c + j];
     vsc[j] = a > 0.f ? 448.f / a : 0.f;
   }
-  u32x4 kraw[4], vraw[4];
+  u32x4 kraw[NI], vraw[NI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = k0 + r0 + 16 * i;
+  for (int i = 0; i < NI; ++i) {
+    const int64_t row = k0 + r0 + RPP * i;
     kraw[i] = vraw[i] = u32x4{0, 0, 0, 0};
     if (row < p.Skv) {
       const int64_t g = row * p.kv_stride + int64_t(h) * D + c;
@@ -269,10 +276,10 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
     }
   }
   // K: x' = bf16(x) - mean (rows >= Skv are 0), amax over the tile
-  float x[4][8], am = 0.f;
+  float x[NI][8], am = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = k0 + r0 + 16 * i;
+  for (int i = 0; i < NI; ++i) {
+    const int64_t row = k0 + r0 + RPP * i;
     const bool ok = row < p.Skv;
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[i][j] = bf2f(uint16_t(kraw[i][j >> 1] >> ((j & 1) * 16)));
@@ -285,8 +292,8 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
   }
   // V -> e4m3 into the transposed LDS tile while the K amax reduces
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int key = r0 + 16 * i;
+  for (int i = 0; i < NI; ++i) {
+    const int key = r0 + RPP * i;
     const bool ok = k0 + key < p.Skv;
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
@@ -303,8 +310,8 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
   am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float inv = am > 0.f ? 127.f / am : 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    *reinterpret_cast<u32x2*>(ki + (int64_t(h) * skv_pad + k0 + r0 + 16 * i) * D + c) = quant8(x[i], inv);
+  for (int i = 0; i < NI; ++i)
+    *reinterpret_cast<u32x2*>(ki + (int64_t(h) * skv_pad + k0 + r0 + RPP * i) * D + c) = quant8(x[i], inv);
   if (tid == 0) ks[int64_t(h) * (skv_pad / kKvPad) + blockIdx.x] = am / 127.f * 1.f;
   // tile table of the attention kernel: liveness bits of the tile's 64 keys (mask and
   // tail) and its K scale
@@ -355,17 +362,17 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
 // and a neighbouring MFMA wave slows it by a further 20-30%.
 
 constexpr int KT = 64;
-constexpr int KTILEB = KT * D;        // 8 KB int8 K tile
-constexpr int VTILEB = D * KT;        // 8 KB fp8 V^T tile
-constexpr int STAGEB = KTILEB + VTILEB;
-// Split partial of one work-group of NW waves (see sage_plan): acc as [NW waves]
-// [16 float4][64 lanes], then m and l as [NW waves][64 lanes][2].
-constexpr int split_acc(int nw) { return nw * 16 * 64 * 4; }
-constexpr int split_floats(int nw) { return split_acc(nw) + nw * 64 * 2; }
+constexpr int kPipeD = 128;               // head dimension of sage_attn_pipe
+constexpr int KTILEB = KT * kPipeD;       // 8 KB int8 K tile (D = 128)
+constexpr int VTILEB = kPipeD * KT;       // 8 KB fp8 V^T tile (D = 128)
+// Split partial of one work-group of NW waves at head dimension d (see sage_plan):
+// acc as [NW waves][d/8 float4][64 lanes], then m and l as [NW waves][64 lanes][2].
+constexpr int split_acc(int nw, int d) { return nw * (d / 8) * 64 * 4; }
+constexpr int split_floats(int nw, int d) { return split_acc(nw, d) + nw * 64 * 2; }
 constexpr int kMaxParts = 4;  // bounds the merge's reads (parts x 132 KB per unit)
 struct SageSplit {
   int full, parts;  // work-groups [0, full) run whole units; the rest run one of `parts` key ranges
-  float* part;      // partials, split_floats(NW) per split work-group
+  float* part;      // partials, split_floats(NW, D) per split work-group
   int* cnt;         // arrival counter per split unit
 };
 constexpr float kSageHeadroom = 2.f;
@@ -373,9 +380,7 @@ constexpr int kScoreBias = 0x4B400000;  // bits of 12582912.0f = 1.5 * 2^23
 constexpr i32x16 kScoreBias16 = {kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
                                  kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
                                  kScoreBias, kScoreBias, kScoreBias, kScoreBias};
-#ifndef MXA_SAGE_NS
-#define MXA_SAGE_NS 2
-#endif
+constexpr int kSageStages = 2;  // K/V stages of sage_attn_gen (3 and 4 measured no faster)
 
 // Online-softmax step of one lane over the 32 biased int32 scores of a tile
 // (reference attention_fp8.cu:306-345): integer row max, sc = qs * ks, one FMA into
@@ -439,18 +444,21 @@ __device__ __forceinline__ int kperm(int kb, int m) {
   return ((m >> 2) & 1) * 32 + kb * 16 + (m >> 3) * 4 + (m & 3);
 }
 
-// DMA of one tile (K 8 KB + V^T 8 KB, 8 ops of 1 KB each) by NW waves; op j:
-// K rows (j&1)*32 + lane/2 of d-chunk j/2 (16-byte half XOR row bit 5), V^T
-// channel rows j*16 + lane/4 (16-byte chunk XOR ((row >> 2) & 3)); wave w issues
-// ops j = jj*NW + w. Per-head buffer resources; the per-lane part of each address
-// is loop-invariant (NW even, so j&1 == w&1), the tile and op parts are scalar.
+// DMA of one tile (K and V^T, D/16 ops of 1 KB each) by the eight waves of sage_attn_gen;
+// K op j: rows (j&1)*32 + lane/2 of d-chunk j/2 (16-byte half XOR row bit 5); V^T op j:
+// channel rows j*16 + lane/4 (16-byte chunk XOR ((row >> 2) & 3)). D = 128: wave w
+// issues K op w and V^T op w; D = 64: waves 0..3 issue K op w, waves 4..7 V^T op w-4.
+// Per-head buffer resources; the per-lane part of each address is loop-invariant (it
+// depends on j only through j&1 == w&1), the tile and op parts are scalar.
+template <int D>
 struct SageAddr {
   __amdgpu_buffer_rsrc_t rk, rv;
   uint32_t lk, lv;  // per-lane byte offsets
 };
-__device__ __forceinline__ SageAddr sage_addr(const int8_t* ki, const uint8_t* vt, int kvh, int64_t skv_pad, int wave,
-                                              int lane) {
-  SageAddr a;
+template <int D>
+__device__ __forceinline__ SageAddr<D> sage_addr(const int8_t* ki, const uint8_t* vt, int kvh, int64_t skv_pad,
+                                                 int wave, int lane) {
+  SageAddr<D> a;
   a.rk = buf_rsrc(ki + int64_t(kvh) * skv_pad * D, uint32_t(skv_pad * D));
   a.rv = buf_rsrc(vt + int64_t(kvh) * D * skv_pad, uint32_t(skv_pad * D));
   const int krow = (wave & 1) * 32 + (lane >> 1);
@@ -459,30 +467,33 @@ __device__ __forceinline__ SageAddr sage_addr(const int8_t* ki, const uint8_t* v
   a.lv = uint32_t(vrow) * uint32_t(skv_pad) + uint32_t(((lane & 3) ^ ((vrow >> 2) & 3)) << 4);
   return a;
 }
+// DMA ops per wave per tile.
+template <int D>
+constexpr int sage_ops_per_wave() { return D / 64; }
 // K tile tk into kdst and V^T tile tv into vdst.
-template <int NW>
-__device__ __forceinline__ void sage_load_tile(const SageAddr& a, int tk, int tv, unsigned char* kdst,
+template <int D>
+__device__ __forceinline__ void sage_load_tile(const SageAddr<D>& a, int tk, int tv, unsigned char* kdst,
                                                unsigned char* vdst, int wave, int64_t skv_pad) {
-  static_for<8 / NW>([&](auto jjc) __attribute__((always_inline)) {
-    const int j = decltype(jjc)::value * NW + wave;
+  auto kop = [&](int j) __attribute__((always_inline)) {
     buf2lds16(a.rk, a.lk, uint32_t((j >> 1) * 32 + tk * (KT * D)), (MXA_LDS void*)(kdst + j * 1024));
+  };
+  auto vop = [&](int j) __attribute__((always_inline)) {
     buf2lds16(a.rv, a.lv, uint32_t(j * 16) * uint32_t(skv_pad) + uint32_t(tv * KT), (MXA_LDS void*)(vdst + j * 1024));
-  });
-}
-// K tile tk only.
-template <int NW>
-__device__ __forceinline__ void sage_load_k(const SageAddr& a, int tk, unsigned char* kdst, int wave) {
-  static_for<8 / NW>([&](auto jjc) __attribute__((always_inline)) {
-    const int j = decltype(jjc)::value * NW + wave;
-    buf2lds16(a.rk, a.lk, uint32_t((j >> 1) * 32 + tk * (KT * D)), (MXA_LDS void*)(kdst + j * 1024));
-  });
+  };
+  if constexpr (D == 128) {
+    kop(wave);
+    vop(wave);
+  } else {
+    if (wave < 4) kop(wave);
+    else vop(wave - 4);
+  }
 }
 
 // End of a work-group: a split part publishes (acc, m, l) and returns unless it is
 // the last of its unit to arrive, which merges every part; then O = acc * vamax[d] /
 // (448 l) -> bf16 for this lane's query row.
-template <int NW>
-__device__ __forceinline__ void sage_finish(f32x16 (&acc)[4], float m, float l, int part, int su, const SageSplit& sp,
+template <int NW, int D>
+__device__ __forceinline__ void sage_finish(f32x16 (&acc)[D / 32], float m, float l, int part, int su, const SageSplit& sp,
                                             int wave, int lane, int row, const mx_attn_params& p,
                                             const float* __restrict__ va, int kvh, int head,
                                             uint16_t* __restrict__ o) {
@@ -493,14 +504,14 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[4], float m, float l, 
     // XCDs' non-coherent L2s for these lines only; a device-scope fence would write
     // back and invalidate a whole L2 and with it every other work-group's K/V.
     constexpr int kSc1 = 16;  // cache policy: device scope
-    constexpr int kSplitAcc = split_acc(NW), kSplitFloats = split_floats(NW);
+    constexpr int kSplitAcc = split_acc(NW, D), kSplitFloats = split_floats(NW, D);
     const uint32_t unit_bytes = uint32_t(sp.parts) * kSplitFloats * 4;
     const __amdgpu_buffer_rsrc_t rp = buf_rsrc(sp.part + int64_t(su) * sp.parts * kSplitFloats, unit_bytes);
-    const uint32_t lacc = uint32_t(wave * 16 * 64 + lane) * 16u;          // + j * 1024 for float4 j
+    const uint32_t lacc = uint32_t(wave * (D / 8) * 64 + lane) * 16u;     // + j * 1024 for float4 j
     const uint32_t lml = uint32_t(kSplitAcc + (wave * 64 + lane) * 2) * 4u;
     const uint32_t mine = uint32_t(part) * kSplitFloats * 4u;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < D / 32; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
         __builtin_amdgcn_raw_buffer_store_b128(
@@ -533,19 +544,19 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[4], float m, float l, 
     }
     l = 0.f;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
+    for (int db = 0; db < D / 32; ++db) acc[db] = f32x16{};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       if (i >= sp.parts) break;
       const float wi = mm == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(mi[i] - mm);
       l += li[i] * wi;
-      f32x4 x[16];
+      f32x4 x[D / 8];
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
+      for (int j = 0; j < D / 8; ++j)
         x[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                             rp, lacc + uint32_t(j) * 1024u, uint32_t(i) * kSplitFloats * 4u, kSc1));
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
+      for (int j = 0; j < D / 8; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[j >> 2][(j & 3) * 4 + e] += x[j][e] * wi;
     }
@@ -556,7 +567,7 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[4], float m, float l, 
     const float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
     uint16_t* dst = o + int64_t(row) * p.o_stride + head * D + h * 4;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < D / 32; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = db * 32 + g * 8 + h * 4;
@@ -568,13 +579,15 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[4], float m, float l, 
   }
 }
 
-template <int NS>
+template <int D, int NS>
 __global__ void __launch_bounds__(512, 1)
-sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, const uint8_t* __restrict__ vt,
+sage_attn_gen(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, const uint8_t* __restrict__ vt,
                const float* __restrict__ qs, const float* __restrict__ ks, const float* __restrict__ va,
                uint16_t* __restrict__ o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad, SageSplit sp) {
-  constexpr int NW = 8, QT = NW * 32, OPS = 2 * (8 / NW);
+  constexpr int NW = 8, QT = NW * 32, OPS = sage_ops_per_wave<D>(), NC = D / 32;
+  constexpr int KTB = KT * D, STAGEB = 2 * KT * D;  // K tile, then V^T tile
   static_assert(NS >= 2 && NS <= 4, "2..4 stages");
+  static_assert(D == 64 || D == 128, "head dimension 64 or 128");
   __shared__ __align__(16) unsigned char st0[STAGEB];
   __shared__ __align__(16) unsigned char st1[STAGEB];
   __shared__ __align__(16) unsigned char st2[STAGEB];
@@ -610,9 +623,9 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   const int q0 = qtile * QT + wave * 32;
 
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const SageAddr sa = sage_addr(ki, vt, kvh, skv_pad, wave_u, lane);
+  const SageAddr<D> sa = sage_addr<D>(ki, vt, kvh, skv_pad, wave_u, lane);
   auto issue = [&](int t, unsigned char* dst) __attribute__((always_inline)) {
-    sage_load_tile<NW>(sa, t, t, dst, dst + KTILEB, wave_u, skv_pad);
+    sage_load_tile<D>(sa, t, t, dst, dst + KTB, wave_u, skv_pad);
   };
   issue(tb, stage(std::integral_constant<int, 0>{}));
   if constexpr (NS > 2) if (tb + 1 < nt) issue(tb + 1, stage(std::integral_constant<int, 1>{}));
@@ -620,11 +633,11 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
 
   // Q^T fragments: lane (n, h) holds 16 int8 channels 32c + 16h .. +15 of its query.
   const int row = q0 + n;  // < sq_pad (sq_pad is a multiple of QT)
-  i32x4 qf[4];
+  i32x4 qf[NC];
   {
     const int8_t* src = qi + (int64_t(head) * sq_pad + row) * D + h * 16;
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) qf[cc] = *reinterpret_cast<const i32x4*>(src + cc * 32);
+    for (int cc = 0; cc < NC; ++cc) qf[cc] = *reinterpret_cast<const i32x4*>(src + cc * 32);
   }
   const float qscale = qs[int64_t(head) * (sq_pad / 16) + row / 16];
   const float* kscale = ks + int64_t(kvh) * (skv_pad / KT);
@@ -635,12 +648,12 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   const int krow = kperm(0, n);
   const int kbase = krow * 32 + ((h ^ ((krow >> 5) & 1)) << 4);
   const int vsw = (n >> 2) & 3;
-  const int vbase0 = KTILEB + n * 64 + (((2 * h) ^ vsw) << 4);
-  const int vbase1 = KTILEB + n * 64 + (((2 * h + 1) ^ vsw) << 4);
+  const int vbase0 = KTB + n * 64 + (((2 * h) ^ vsw) << 4);
+  const int vbase1 = KTB + n * 64 + (((2 * h + 1) ^ vsw) << 4);
 
-  f32x16 acc[4];
+  f32x16 acc[NC];
 #pragma unroll
-  for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
+  for (int db = 0; db < NC; ++db) acc[db] = f32x16{};
   float m = -__builtin_inff(), l = 0.f;
 
   auto step = [&](int t, auto i) __attribute__((always_inline)) {
@@ -656,7 +669,7 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
     // ---- S^T = K Q^T (int32, exact) ----
     i32x16 s[2];
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc)
+    for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const i32x4 a = *reinterpret_cast<const i32x4*>(sd + kbase + cc * 2048 + kb * 512);
@@ -664,34 +677,38 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
         // exactly 12582912 + s (|s| < 2^22), so no int->float conversion is needed
         s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[cc], cc == 0 ? kScoreBias16 : s[kb], 0, 0, 0);
       }
-    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    if constexpr (D == 128) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (j == 1 || j == 4) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      if (j < 5) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int j = 0; j < 8; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (j == 1 || j == 4) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        if (j < 5) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
     }
 
     i32x8 pf;
     const float alpha = sage_softmax(s, live, h, fmaxf(qscale * ksc, 1e-30f), m, l, pf);
     if (!__all(alpha == 1.f)) {
 #pragma unroll
-      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+      for (int db = 0; db < NC; ++db) acc[db] *= alpha;
     }
 
     // ---- O^T += V^T P^T (e4m3 x e4m3 -> fp32) ----
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < NC; ++db) {
       const i32x4 a0 = *reinterpret_cast<const i32x4*>(sd + vbase0 + db * 2048);
       const i32x4 a1 = *reinterpret_cast<const i32x4*>(sd + vbase1 + db * 2048);
       const i32x8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
       acc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, pf, acc[db], 0, 0, 0, 0, 0, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    if constexpr (D == 128) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (j < 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      for (int j = 0; j < 4; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (j < 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
     }
   };
   for (int t = tb; t < nt; t += NS) {
@@ -702,13 +719,13 @@ sage_attn_d128(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   }
 
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
-  sage_finish<NW>(acc, m, l, part, su, sp, wave, lane, row, p, va, kvh, head, o);
+  sage_finish<NW, D>(acc, m, l, part, su, sp, wave, lane, row, p, va, kvh, head, o);
 }
 
 // ---------------- software-pipelined main kernel ----------------
 //
 // Same work-group shape, unit/split mapping, LDS tile layouts and arithmetic as
-// sage_attn_d128, but each wave overlaps its own matrix and vector work: in the
+// sage_attn_gen<128>, but each wave overlaps its own matrix and vector work: in the
 // iteration of tile t it runs the online softmax of S(t) while it issues the score
 // MFMAs of S(t+1) and the P(t-1) V(t-1) MFMAs, and it ends with the row max of S(t+1)
 // and the LDS operands of iteration t+1 already in registers. The whole tile loop is
@@ -734,7 +751,7 @@ __global__ void __launch_bounds__(256, 2)
 sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, const uint8_t* __restrict__ vt_g,
                const float* __restrict__ qs, const u32x4* __restrict__ tab_g, const float* __restrict__ va,
                uint16_t* __restrict__ o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad, SageSplit sp) {
-  constexpr int NW = kPipeWaves, QT = NW * 32;
+  constexpr int NW = kPipeWaves, QT = NW * 32, D = kPipeD;
   __shared__ __align__(16) unsigned char kring[4 * KTILEB];
   __shared__ __align__(16) unsigned char vring[4 * VTILEB];
   __shared__ __align__(16) u32x4 table[kPipeMaxTiles + 1];
@@ -744,7 +761,7 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   int L, tb = 0, nt = nkt, su = 0, part = -1;
   if (int(blockIdx.x) < sp.full) {
     L = xcd_remap(blockIdx.x, sp.full);
-  } else {  // split units, part-major (see sage_attn_d128)
+  } else {  // split units, part-major (see sage_attn_gen)
     const int j = int(blockIdx.x) - sp.full, nsu = (int(gridDim.x) - sp.full) / sp.parts;
     part = j / nsu;
     su = j - part * nsu;
@@ -918,21 +935,22 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
   f32x16 acc[4] = {acc0, acc1, acc2, acc3};
   l += other_half(l);  // the wave halves summed different keys of the same rows
-  sage_finish<NW>(acc, m, l, part, su, sp, wave, lane, row, p, va, kvh, head, o);
+  sage_finish<NW, D>(acc, m, l, part, su, sp, wave, lane, row, p, va, kvh, head, o);
 }
 
 }  // namespace
 
 // Workspace carve-up (kept in one place for the host code and the kernels).
 // Two main kernels: sage_attn_pipe (4 waves, 128 queries per work-group, two
-// work-groups per CU; key tiles up to kPipeMaxTiles) and sage_attn_d128 (8 waves, 256
-// queries, one work-group per CU; any length). The choice depends on Skv only.
+// work-groups per CU; D = 128, key tiles up to kPipeMaxTiles) and sage_attn_gen (8
+// waves, 256 queries, one work-group per CU; D = 64 or 128, any length). The choice
+// depends on D and Skv only.
 struct SageShape {
   bool pipe;
   int qt, nw, per_cu;
 };
 SageShape sage_shape(const mx_attn_params& p) {
-  const bool pipe = (p.Skv + KT - 1) / KT <= kPipeMaxTiles;
+  const bool pipe = p.D == kPipeD && (p.Skv + KT - 1) / KT <= kPipeMaxTiles;
   return pipe ? SageShape{true, kPipeWaves * 32, kPipeWaves, 2} : SageShape{false, 256, 8, 1};
 }
 
@@ -994,18 +1012,19 @@ mx_sage_layout sage_layout(const mx_attn_params& p) {
   L.va = take(sizeof(float) * p.Hkv * p.D);
   L.part = take(sizeof(float) * 2 * p.Hkv * nb * p.D);
   L.tab = take(16 * size_t(p.Hkv) * size_t(L.skv_pad / kKvPad + 1));
-  L.split = take(sizeof(float) * split_floats(sage_shape(p).nw) * size_t(pl.units) * pl.parts);
+  L.split = take(sizeof(float) * split_floats(sage_shape(p).nw, p.D) * size_t(pl.units) * pl.parts);
   L.cnt = take(sizeof(int) * size_t(pl.units));
   L.total = off;
   return L;
 }
 
-// Prologue: preconditions checked by the caller (D == 128, q/k/v 16-byte aligned,
+// Prologue: preconditions checked by the caller (D == 64 or 128, q/k/v 16-byte aligned,
 // strides % 8 == 0, ws 256-byte aligned and large enough).
 // nr: null for the plain prologue, else {Q norm/rope, K norm/rope} applied on the fly
 // (D == 128 and nr128_supported, checked by the caller).
-hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint16_t* v, const mx_attn_params& p,
-                                char* ws, hipStream_t s, const NormRope* nr, int q_group) {
+template <int D>
+hipError_t sage_quantize_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, const mx_attn_params& p,
+                           char* ws, hipStream_t s, const NormRope* nr, int q_group) {
   const mx_sage_layout L = sage_layout(p);
   const int nb = (p.Skv + kStatTok - 1) / kStatTok;
   float* part = reinterpret_cast<float*>(ws + L.part);
@@ -1021,11 +1040,19 @@ hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint
   // the Q work-groups hold four consecutive 16-row groups of one head (sq_pad is a
   // multiple of 64), i.e. one 64-row block, for the QG = 64 variant
   static_assert(kSqPad % 64 == 0, "Q padding must cover whole 64-row blocks");
-  auto stats = q_group == 64 ? prep_stats_q<-1, 64>
-             : mode < 0 ? prep_stats_q<-1, 16> : mode == kRopeNone ? prep_stats_q<kRopeNone, 16>
-             : mode == kRopeInterleaved ? prep_stats_q<kRopeInterleaved, 16> : prep_stats_q<kRopeHalf, 16>;
-  auto kvq = mode < 0 ? prep_kv_quant<-1> : mode == kRopeNone ? prep_kv_quant<kRopeNone>
-           : mode == kRopeInterleaved ? prep_kv_quant<kRopeInterleaved> : prep_kv_quant<kRopeHalf>;
+  decltype(&prep_stats_q<D, -1, 16>) stats;
+  decltype(&prep_kv_quant<D, -1>) kvq;
+  if constexpr (D == 128) {
+    stats = q_group == 64 ? prep_stats_q<D, -1, 64>
+          : mode < 0 ? prep_stats_q<D, -1, 16> : mode == kRopeNone ? prep_stats_q<D, kRopeNone, 16>
+          : mode == kRopeInterleaved ? prep_stats_q<D, kRopeInterleaved, 16> : prep_stats_q<D, kRopeHalf, 16>;
+    kvq = mode < 0 ? prep_kv_quant<D, -1> : mode == kRopeNone ? prep_kv_quant<D, kRopeNone>
+        : mode == kRopeInterleaved ? prep_kv_quant<D, kRopeInterleaved> : prep_kv_quant<D, kRopeHalf>;
+  } else {
+    if (mode >= 0) return hipErrorInvalidValue;  // the fused norm/rope prologue is D = 128 only
+    stats = q_group == 64 ? prep_stats_q<D, -1, 64> : prep_stats_q<D, -1, 16>;
+    kvq = prep_kv_quant<D, -1>;
+  }
   hipLaunchKernelGGL(stats, dim3(unsigned(blocks1)), dim3(256), 0, s, q, k, v, p, nb, qmult, L.sq_pad, part,
                      reinterpret_cast<int8_t*>(ws + L.qi), reinterpret_cast<float*>(ws + L.qs), nq, nk);
   // up to kFoldNb statistics partials per head (Skv <= 8192) the K/V quantizer sums
@@ -1033,13 +1060,20 @@ hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint
   // re-reading would outweigh the separate prep_finalize launch
   const int fold = nb <= kFoldNb ? nb : 0;
   if (!fold)
-    hipLaunchKernelGGL(prep_finalize, dim3(p.Hkv), dim3(D), 0, s, p, nb, (const float*)part, km, va,
+    hipLaunchKernelGGL(prep_finalize<D>, dim3(p.Hkv), dim3(D), 0, s, p, nb, (const float*)part, km, va,
                        reinterpret_cast<int*>(ws + L.cnt), L.split_units);
   hipLaunchKernelGGL(kvq, dim3(unsigned(L.skv_pad / kKvPad), p.Hkv), dim3(256), 0, s, k, v, p, L.skv_pad, km, va,
                      reinterpret_cast<int8_t*>(ws + L.ki), reinterpret_cast<float*>(ws + L.ks),
                      reinterpret_cast<uint8_t*>(ws + L.vt), nk, fold, (const float*)part,
                      reinterpret_cast<int*>(ws + L.cnt), L.split_units, reinterpret_cast<u32x4*>(ws + L.tab));
   return hipGetLastError();
+}
+
+hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint16_t* v, const mx_attn_params& p,
+                                char* ws, hipStream_t s, const NormRope* nr, int q_group) {
+  if (p.D == 128) return sage_quantize_d<128>(q, k, v, p, ws, s, nr, q_group);
+  if (p.D == 64) return sage_quantize_d<64>(q, k, v, p, ws, s, nr, q_group);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_sage_attend(uint16_t* o, const mx_attn_params& p, const char* ws, hipStream_t s) {
@@ -1061,9 +1095,14 @@ hipError_t launch_sage_attend(uint16_t* o, const mx_attn_params& p, const char* 
   if (sh.pipe)
     hipLaunchKernelGGL(sage_attn_pipe, dim3(unsigned(blocks)), dim3(sh.nw * 64), 0, s, qi, ki, vt, qs,
                        reinterpret_cast<const u32x4*>(ws + L.tab), va, o, p, L.sq_pad, L.skv_pad, sp);
+  else if (p.D == 128)
+    hipLaunchKernelGGL((sage_attn_gen<128, kSageStages>), dim3(unsigned(blocks)), dim3(sh.nw * 64), 0, s, qi, ki, vt,
+                       qs, reinterpret_cast<const float*>(ws + L.ks), va, o, p, L.sq_pad, L.skv_pad, sp);
+  else if (p.D == 64)
+    hipLaunchKernelGGL((sage_attn_gen<64, kSageStages>), dim3(unsigned(blocks)), dim3(sh.nw * 64), 0, s, qi, ki, vt,
+                       qs, reinterpret_cast<const float*>(ws + L.ks), va, o, p, L.sq_pad, L.skv_pad, sp);
   else
-    hipLaunchKernelGGL(sage_attn_d128<MXA_SAGE_NS>, dim3(unsigned(blocks)), dim3(sh.nw * 64), 0, s, qi, ki, vt, qs,
-                       reinterpret_cast<const float*>(ws + L.ks), va, o, p, L.sq_pad, L.skv_pad, sp);
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

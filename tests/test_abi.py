@@ -139,3 +139,26 @@ def test_sage_tile_loop_is_generated():
     spec.loader.exec_module(gen)
     with open(os.path.join(ROOT, "miroxen_amd", "csrc", "sage_tile.inc")) as f:
         assert f.read() == gen.generate()
+
+
+def test_fp8_ok_rejects_keys_past_32bit_offsets():
+    """The quantized kernels address a K/V head through 32-bit buffer offsets: a head of
+    skv_pad * D >= 2^32 bytes is not taken (the caller falls back to flash_attn). The
+    decision is made before any device query, so it holds without a GPU."""
+    from miroxen_amd.attention import flash_attn_fp8_ok
+    for D, skv in ((128, 2 ** 25), (64, 2 ** 26), (128, 2 ** 25 + 1)):
+        p = AttnParams(Sq=64, Skv=skv, Hq=1, Hkv=1, D=D)
+        assert not flash_attn_fp8_ok(256, 256, 256, 256, p)
+
+
+def test_workspace_layout_d64():
+    """D = 64 runs the 8-wave kernel (256-query units): config-2 shape at D = 64 has 408
+    units on 256 slots, so its last 152 units are split; the partials are sized for
+    D = 64 (8 waves x (8 float4 of acc + m, l) x 64 lanes)."""
+    p = AttnParams(Sq=4352, Skv=4352, Hq=24, Hkv=24, D=64)
+    L = sage_layout(p)
+    assert L["split_qt"] == 256 and L["split_units"] == 152 and L["split_parts"] > 1
+    assert L["ki"] == 24 * 4352 * 64 and L["vt"] == 2 * 24 * 4352 * 64
+    per_wg = 4 * (8 * 8 * 64 * 4 + 8 * 64 * 2)
+    assert L["cnt"] - L["split"] >= per_wg * L["split_units"] * L["split_parts"]
+    assert L["cnt"] - L["split"] < per_wg * L["split_units"] * L["split_parts"] + 256

@@ -71,13 +71,14 @@ def test_supported(cuda):
     assert flash_attn_fp8_supported(0)
 
 
-@pytest.mark.parametrize("Sq,Skv,Hq,Hkv,pad,kbias", [
-    (1, 1, 1, 1, 0, 0.0), (300, 300, 4, 4, 0, 0.0), (257, 1000, 4, 2, 0, 4.0), (130, 77, 2, 2, 8, 2.0),
-    (1088, 1088, 24, 24, 0, 8.0),
+@pytest.mark.parametrize("Sq,Skv,Hq,Hkv,D,pad,kbias", [
+    (1, 1, 1, 1, 128, 0, 0.0), (300, 300, 4, 4, 128, 0, 0.0), (257, 1000, 4, 2, 128, 0, 4.0),
+    (130, 77, 2, 2, 128, 8, 2.0), (1088, 1088, 24, 24, 128, 0, 8.0),
+    (1, 1, 1, 1, 64, 0, 0.0), (300, 300, 4, 4, 64, 0, 0.0), (257, 1000, 4, 2, 64, 0, 4.0),
+    (130, 77, 2, 2, 64, 8, 2.0), (1088, 1088, 24, 24, 64, 0, 8.0),
 ])
-def test_prologue_bit_exact(cuda, Sq, Skv, Hq, Hkv, pad, kbias):
-    D = 128
-    print(f"prologue {Sq}x{Skv} H={Hq}/{Hkv} pad={pad}", flush=True)
+def test_prologue_bit_exact(cuda, Sq, Skv, Hq, Hkv, D, pad, kbias):
+    print(f"prologue {Sq}x{Skv} H={Hq}/{Hkv} D={D} pad={pad}", flush=True)
     q, k, v, qs, ks = _bias_inputs(Sq, Skv, Hq, Hkv, D, pad, kbias, cuda, Sq * 31 + Skv)
     p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=D, q_stride=qs, kv_stride=ks, o_stride=qs)
     ws = _ws(p, cuda)
@@ -135,18 +136,23 @@ def test_q_group_64_config3(cuda):
     emu = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128, kv_valid=mk,
                               rows=rows, headroom=oracle.KERNEL_HEADROOM,
                               split=(units - L["split_units"], L["split_parts"], L["split_qt"]))
+    ref_rule = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128,
+                                   kv_valid=mk, rows=rows, headroom=0.0)
     exact = oracle.attention_f64(_bits(q), _bits(k), _bits(v), S, S, H, H, 128, kv_valid=mk, rows=rows)
     got = _f32(o[torch.from_numpy(rows).long().to(cuda)])
     c_emu, c_ex, rr = cosine(got, emu), cosine(got, exact), rel_rms(got, exact)
-    print(f"config3 q_group=64: cos(emu)={c_emu:.7f} cos(exact)={c_ex:.6f} relrms={rr:.4f}", flush=True)
-    assert c_emu >= 0.99999 and c_ex >= 0.995 and rr < 0.045
+    rr_ref = rel_rms(ref_rule, exact)
+    print(f"config3 q_group=64: cos(emu)={c_emu:.7f} cos(exact)={c_ex:.6f} relrms={rr:.4f} "
+          f"relrms(reference rule)={rr_ref:.4f}", flush=True)
+    # the gate of _sage_vs_oracle: 4 %, or the reference arithmetic's own figure + 0.25 points
+    assert c_emu >= 0.99999 and c_ex >= 0.995 and rr < max(0.04, rr_ref + 0.0025)
 
 
-@pytest.mark.parametrize("Sq,Skv,Hq,Hkv,pad", [(300, 300, 4, 4, 0), (130, 517, 4, 2, 8), (64, 64, 2, 2, 0)])
-def test_q_group_64_prologue_bit_exact(cuda, Sq, Skv, Hq, Hkv, pad):
+@pytest.mark.parametrize("Sq,Skv,Hq,Hkv,D,pad", [(300, 300, 4, 4, 128, 0), (130, 517, 4, 2, 128, 8),
+                                              (64, 64, 2, 2, 128, 0), (130, 517, 4, 2, 64, 8)])
+def test_q_group_64_prologue_bit_exact(cuda, Sq, Skv, Hq, Hkv, D, pad):
     """Q per 64 tokens on small shapes: a partial last 64-row block (rows past Sq count
     as zeros), GQA, padded strides; every workspace region against the oracle with G = 64."""
-    D = 128
     print(f"q_group=64 prologue {Sq}x{Skv} H={Hq}/{Hkv} pad={pad}", flush=True)
     q, k, v, qs, ks = _bias_inputs(Sq, Skv, Hq, Hkv, D, pad, 2.0, cuda, Sq * 13 + Skv)
     p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=D, q_stride=qs, kv_stride=ks, o_stride=qs)
@@ -186,14 +192,17 @@ def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
     got = _f32(o[torch.from_numpy(rows).long().to(cuda)])
     c_emu, e_emu = cosine(got, emu), max_abs(got, emu)
     c_ex, rr = cosine(got, exact), rel_rms(got, exact)
-    print(f"{seed_note} sage: cos(emu)={c_emu:.7f} maxabs(emu)={e_emu:.3g} cos(exact)={c_ex:.6f} relrms={rr:.4f}",
-          flush=True)
+    rr_ref = rel_rms(ref_rule, exact)
+    print(f"{seed_note} sage: cos(emu)={c_emu:.7f} maxabs(emu)={e_emu:.3g} cos(exact)={c_ex:.6f} relrms={rr:.4f} "
+          f"relrms(reference rule)={rr_ref:.4f}", flush=True)
     # emulator fed the same workspace: only accumulation order and the bf16 store differ
     assert c_emu >= 0.99999 and e_emu <= 2e-2
-    # BASELINE bar for Sage vs FP32: cosine >= 0.995. The reference's own 4 % rel-RMS
-    # gate is applied to its own cases (test_reference_sage_cases); the configs here
-    # include the K-outlier stress case, held to 4.5 %.
-    assert c_ex >= 0.995 and rr < 0.045
+    # Cosine >= 0.995 against exact attention, and the reference's 4 % rel-RMS gate
+    # (tests/attention_fp8_test.cpp:65) unless the reference's own arithmetic (exact-max
+    # emulator on the same quantized operands) already exceeds it on this input: then
+    # the kernel is held to that figure plus 0.25 points.
+    assert c_ex >= 0.995
+    assert rr < max(0.04, rr_ref + 0.0025), (rr, rr_ref)
     return o
 
 
@@ -211,11 +220,12 @@ def test_sage_configs(cuda, cfg_id):
     (1024, 4352, 2, 2, 128, 0, 8.0),
 ])
 def test_reference_sage_cases(cuda, Sq, Skv, Hq, Hkv, D, pad, kbias):
-    """The reference's four Sage cases (tests/attention_fp8_test.cpp:110-113): rel-RMS < 4 %
-    against exact attention. D=64 takes the flash_attn fallback in this build."""
+    """The reference's four Sage cases (tests/attention_fp8_test.cpp:110-113), D = 64
+    included, all on the quantized path: rel-RMS < 4 % against exact attention."""
     q, k, v, qs, ks = _bias_inputs(Sq, Skv, Hq, Hkv, D, pad, kbias, cuda, Sq * 31 + Skv)
     p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=D, q_stride=qs if pad else 0, kv_stride=ks if pad else 0,
                    o_stride=qs if pad else 0)
+    assert flash_attn_fp8_ok(q, k, v, q, p)
     ws = _ws(p, cuda)
     o = torch.zeros(Sq * qs, dtype=torch.bfloat16, device=cuda)
     flash_attn_fp8(q, k, v, o, p, ws)
@@ -240,7 +250,8 @@ def test_fallbacks_and_aliasing(cuda):
     assert flash_attn_fp8_ok(q, k, v, o, p)
     assert not flash_attn_fp8_ok(q, k, v, o, AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128, causal=1))
     assert not flash_attn_fp8_ok(q, k, v, o, AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128, scale=-0.1))
-    assert not flash_attn_fp8_ok(q, k, v, o, AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=64))
+    assert flash_attn_fp8_ok(q, k, v, o, AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=64))
+    assert not flash_attn_fp8_ok(q, k, v, o, AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=72))
     # o aliasing q: same result as a separate output
     ws = _ws(p, cuda)
     sep = torch.empty_like(q)
@@ -296,3 +307,48 @@ def test_split_units_dead_parts_and_repeat(cuda):
     exact = oracle.attention_f64(_bits(q), _bits(k), _bits(v), Sq, Skv, H, H, 128, kv_valid=mask.cpu().numpy())
     got = _f32(outs[0]).reshape(exact.shape)
     assert cosine(got, exact) >= 0.995 and rel_rms(got, exact) < 0.04
+
+
+@pytest.mark.parametrize("Sq,Skv,Hq,Hkv,pad,kbias,masked", [
+    (130, 77, 2, 2, 8, 2.0, False), (300, 300, 4, 4, 0, 0.0, False), (257, 1000, 4, 2, 0, 4.0, True),
+    (4352, 4352, 24, 24, 0, 8.0, True),
+])
+def test_sage_d64(cuda, Sq, Skv, Hq, Hkv, pad, kbias, masked):
+    """Sage at D = 64 (the reference's run<64>, attention_fp8.cu:496-497): the kernel
+    against the emulator fed the same workspace and against exact attention, under the
+    gate of _sage_vs_oracle. The last shape has 408 units of 256 queries, so the
+    grid's last round is split by key range and merged."""
+    D = 64
+    print(f"sage D=64 {Sq}x{Skv} H={Hq}/{Hkv} pad={pad} masked={masked}", flush=True)
+    q, k, v, qs, ks = _bias_inputs(Sq, Skv, Hq, Hkv, D, pad, kbias, cuda, Sq * 7 + Skv)
+    mask = None
+    if masked:
+        g = torch.Generator().manual_seed(Skv)
+        mask = (torch.rand(Skv, generator=g) > 0.2).to(torch.uint8).to(cuda)
+    p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=D, q_stride=qs, kv_stride=ks, o_stride=qs, kv_valid=mask)
+    assert flash_attn_fp8_ok(q, k, v, q, p)
+    L = sage_layout(p)
+    ws = _ws(p, cuda)
+    o = torch.zeros_like(q)
+    flash_attn_fp8(q, k, v, o, p, ws)
+    torch.cuda.synchronize()
+    g = _quantized(ws, p, L)
+    mk = None if mask is None else mask.cpu().numpy()
+    rows = np.array(sorted(set(query_rows(Sq, Hq)) | set(range(0, Sq, max(1, Sq // 40)))), np.int32)
+    units = (Sq + L["split_qt"] - 1) // L["split_qt"] * Hq
+    if Sq == 4352:
+        assert L["split_units"] > 0
+    emu = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], Sq, Skv, Hq, Hkv, D,
+                              kv_valid=mk, rows=rows, headroom=oracle.KERNEL_HEADROOM,
+                              split=(units - L["split_units"], L["split_parts"], L["split_qt"]))
+    ref_rule = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], Sq, Skv, Hq, Hkv, D,
+                                   kv_valid=mk, rows=rows, headroom=0.0)
+    exact = oracle.attention_f64(_bits(q), _bits(k), _bits(v), Sq, Skv, Hq, Hkv, D, q_stride=qs, kv_stride=ks,
+                                 kv_valid=mk, rows=rows)
+    got = _f32(o.view(Sq, qs)[torch.from_numpy(rows).long().to(cuda), : Hq * D]).reshape(exact.shape)
+    c_emu, e_emu = cosine(got, emu), max_abs(got, emu)
+    c_ex, rr, rr_ref = cosine(got, exact), rel_rms(got, exact), rel_rms(ref_rule, exact)
+    print(f"  cos(emu)={c_emu:.7f} maxabs(emu)={e_emu:.3g} cos(exact)={c_ex:.6f} relrms={rr:.4f} "
+          f"relrms(reference rule)={rr_ref:.4f}", flush=True)
+    assert c_emu >= 0.99999 and e_emu <= 2e-2
+    assert c_ex >= 0.995 and rr < max(0.04, rr_ref + 0.0025)
