@@ -72,6 +72,18 @@ int mx_flash_attn_fp8_ok(const void* q, const void* k, const void* v, const void
 int mx_flash_attn_fp8(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
                       void* ws, void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc):
+ * mx_flash_attn_fp8 with the workspace taken from a fixed library-owned device scratch
+ * of 128 MiB (one per device, held until the process ends) instead of an argument.
+ * Allocates nothing. Shapes whose workspace (mx_flash_attn_fp8_workspace) exceeds the
+ * scratch return MX_E_UNSUPPORTED; arguments the quantized path does not take fall
+ * back to mx_flash_attn, as in mx_flash_attn_fp8. Every call on a device shares that
+ * device's scratch: calls that overlap on one device (other streams, other host
+ * threads) race and must be serialised by the caller. */
+int mx_flash_attn_fp8_noalloc(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
+                              void* stream);
+
 /* Reference: mx::attn_reference, src/kernels/attention.h:37-38 (attention.cu:313-348, 419-423).
  * Slow naive GPU attention (fp32 softmax), for tests only. */
 int mx_attn_reference(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,

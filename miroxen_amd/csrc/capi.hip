@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <mutex>
 
 #include "attn_common.hpp"
 #include "norm_rope.hpp"
@@ -122,6 +123,35 @@ bool fast_bf16_ok(const void* q, const void* k, const void* v, const void* o, co
          int64_t(p.Skv) * p.kv_stride * 2 < (int64_t(1) << 32);  // K/V tiles read through 32-bit buffer offsets
 }
 
+// Fixed device scratch of mx_flash_attn_fp8_noalloc: the Sage workspace lives in this
+// file-scope array (one copy per device, held until the process ends) instead of a
+// caller allocation. Host code never passes the array's name to a kernel or a copy:
+// on the host it is a stand-in symbol, and each device's copy is at its own address,
+// looked up once per device with hipGetSymbolAddress (with that device current).
+constexpr size_t kNoAllocScratchBytes = size_t(128) << 20;  // 128 MiB
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+int scratch_of_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "flash_attn_fp8_noalloc");
+  if (dev < 0 || dev >= kMaxDevices) return fail(MX_E_UNSUPPORTED, "flash_attn_fp8_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "flash_attn_fp8_noalloc: scratch address");
+    if (!ptr || !aligned(ptr, 256))
+      return fail(MX_E_HIP, "flash_attn_fp8_noalloc: scratch address not 256-byte aligned");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -211,6 +241,33 @@ int mx_flash_attn_fp8(const void* q, const void* k, const void* v, void* o, cons
   if (rc) return rc;
   return hip_status(mxa::launch_sage_attend(static_cast<uint16_t*>(o), a, static_cast<const char*>(ws), s),
                     "flash_attn_fp8");
+}
+
+int mx_flash_attn_fp8_noalloc(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
+                              void* stream) {
+  mx_attn_params a;
+  int rc = validate(q, k, v, o, p, &a);
+  if (rc) return rc;
+  bool ok = false;
+  rc = fp8_ok(q, k, v, o, a, &ok);
+  if (rc) return rc;
+  if (!ok) return mx_flash_attn(q, k, v, o, p, stream);  // as mx_flash_attn_fp8: no workspace needed
+  const size_t need = mxa::sage_layout(a).total;
+  if (need > kNoAllocScratchBytes)
+    return fail(MX_E_UNSUPPORTED, "flash_attn_fp8_noalloc: workspace of %zu bytes exceeds the %zu-byte scratch",
+                need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  rc = scratch_of_current_device(&ws);
+  if (rc) return rc;
+  // the prologue rewrites every region the attention kernel reads and zeroes the
+  // split arrival counters, so nothing is left over from the previous call
+  auto s = static_cast<hipStream_t>(stream);
+  rc = hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                            static_cast<const uint16_t*>(v), a, static_cast<char*>(ws), s, nullptr, 16),
+                  "flash_attn_fp8_noalloc prologue");
+  if (rc) return rc;
+  return hip_status(mxa::launch_sage_attend(static_cast<uint16_t*>(o), a, static_cast<const char*>(ws), s),
+                    "flash_attn_fp8_noalloc");
 }
 
 int mx_sage_quantize(const void* q, const void* k, const void* v, const mx_attn_params* p, void* ws,
