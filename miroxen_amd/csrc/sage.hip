@@ -365,9 +365,10 @@ constexpr int KT = 64;
 constexpr int kPipeD = 128;               // head dimension of sage_attn_pipe
 constexpr int KTILEB = KT * kPipeD;       // 8 KB int8 K tile (D = 128)
 constexpr int VTILEB = kPipeD * KT;       // 8 KB fp8 V^T tile (D = 128)
-// Split partial of one work-group of NW waves at head dimension d (see sage_plan):
-// acc as [NW waves][d/8 float4][64 lanes], then m and l as [NW waves][64 lanes][2].
-constexpr int split_acc(int nw, int d) { return nw * (d / 8) * 64 * 4; }
+// Split partial of one work-group of NW waves at head dimension d (see sage_plan), in
+// 4-byte words: o = acc / (448 l) in fp16 as [NW waves][d/16 groups of 8][64 lanes],
+// then m and l as [NW waves][64 lanes][2] floats.
+constexpr int split_acc(int nw, int d) { return nw * (d / 16) * 64 * 4; }
 constexpr int split_floats(int nw, int d) { return split_acc(nw, d) + nw * 64 * 2; }
 constexpr int kMaxParts = 4;  // bounds the merge's reads (parts x 132 KB per unit)
 struct SageSplit {
@@ -489,9 +490,10 @@ __device__ __forceinline__ void sage_load_tile(const SageAddr<D>& a, int tk, int
   }
 }
 
-// End of a work-group: a split part publishes (acc, m, l) and returns unless it is
-// the last of its unit to arrive, which merges every part; then O = acc * vamax[d] /
-// (448 l) -> bf16 for this lane's query row.
+// End of a work-group: a split part publishes its normalised output o = acc / (448 l)
+// in fp16 (|o| <= 448(1 + 2^-4): a weighted mean of e4m3 values) with (m, l) and
+// returns unless it is the last of its unit to arrive, which merges every part; then
+// O = acc * vamax[d] / (448 l) -> bf16 for this lane's query row.
 template <int NW, int D>
 __device__ __forceinline__ void sage_finish(f32x16 (&acc)[D / 32], float m, float l, int part, int su, const SageSplit& sp,
                                             int wave, int lane, int row, const mx_attn_params& p,
@@ -499,7 +501,7 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[D / 32], float m, floa
                                             uint16_t* __restrict__ o) {
   const int h = lane >> 5;
   if (part >= 0) {
-    // Split unit: publish (acc, m, l), then the last part to arrive merges all parts.
+    // Split unit: publish (o, m, l), then the last part to arrive merges all parts.
     // The partials move with device-scope (sc1) buffer accesses, which bypass the
     // XCDs' non-coherent L2s for these lines only; a device-scope fence would write
     // back and invalidate a whole L2 and with it every other work-group's K/V.
@@ -507,18 +509,32 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[D / 32], float m, floa
     constexpr int kSplitAcc = split_acc(NW, D), kSplitFloats = split_floats(NW, D);
     const uint32_t unit_bytes = uint32_t(sp.parts) * kSplitFloats * 4;
     const __amdgpu_buffer_rsrc_t rp = buf_rsrc(sp.part + int64_t(su) * sp.parts * kSplitFloats, unit_bytes);
-    const uint32_t lacc = uint32_t(wave * (D / 8) * 64 + lane) * 16u;     // + j * 1024 for float4 j
+    const uint32_t lacc = uint32_t(wave * (D / 16) * 64 + lane) * 16u;    // + j * 1024 for 8-half group j
     const uint32_t lml = uint32_t(kSplitAcc + (wave * 64 + lane) * 2) * 4u;
     const uint32_t mine = uint32_t(part) * kSplitFloats * 4u;
+    const float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
+    auto h2 = [](float a, float b) __attribute__((always_inline)) {
+      return uint32_t(__builtin_bit_cast(uint16_t, _Float16(a))) |
+             (uint32_t(__builtin_bit_cast(uint16_t, _Float16(b))) << 16);
+    };
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(u32x4, f32x4{acc[db][g * 4], acc[db][g * 4 + 1], acc[db][g * 4 + 2], acc[db][g * 4 + 3]}),
-            rp, lacc + uint32_t(db * 4 + g) * 1024u, mine, kSc1);
+    for (int j = 0; j < D / 16; ++j) {  // group j: acc[j / 2][(j & 1) * 8 .. + 7]
+      const f32x16& a = acc[j >> 1];
+      const int b = (j & 1) * 8;
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u32x4{h2(a[b] * inv, a[b + 1] * inv), h2(a[b + 2] * inv, a[b + 3] * inv), h2(a[b + 4] * inv, a[b + 5] * inv),
+                h2(a[b + 6] * inv, a[b + 7] * inv)},
+          rp, lacc + uint32_t(j) * 1024u, mine, kSc1);
+    }
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m, l}), rp, lml, mine, kSc1);
-    wait_vm();  // this lane's partial has reached the device-coherent level
+    // Publication order without a release fence: every lane waits until its sc1
+    // stores are acknowledged by the device-coherent level (vmcnt(0)), the barrier
+    // orders all lanes before lane 0's arrival atomic (agent scope, performed at that
+    // same level), and the merging work-group reads the partials only after it has
+    // seen the last arrival (its loads are issued after the barrier that follows the
+    // atomic, and sc1 loads bypass the non-coherent L2, so no stale line can be hit).
+    // An acq_rel atomic would add an L2 writeback + invalidate of the whole XCD.
+    wait_vm();
     __shared__ int last;
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -530,7 +546,7 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[D / 32], float m, floa
     if (!last) return;
     // merge in part order (every part read back, this one's included, so the result
     // does not depend on which part arrived last): M = max m_i, w_i = 2^(m_i - M),
-    // l = sum l_i w_i, acc = sum acc_i w_i
+    // c_i = l_i w_i, l = sum c_i, acc = sum (448 c_i) o_i
     float mi[8], li[8];
     float mm = -__builtin_inff();
 #pragma unroll
@@ -549,16 +565,21 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[D / 32], float m, floa
     for (int i = 0; i < 8; ++i) {
       if (i >= sp.parts) break;
       const float wi = mm == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(mi[i] - mm);
-      l += li[i] * wi;
-      f32x4 x[D / 8];
+      const float ci = li[i] * wi;
+      l += ci;
+      const float c448 = 448.f * ci;
+      u32x4 x[D / 16];
 #pragma unroll
-      for (int j = 0; j < D / 8; ++j)
-        x[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+      for (int j = 0; j < D / 16; ++j)
+        x[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                             rp, lacc + uint32_t(j) * 1024u, uint32_t(i) * kSplitFloats * 4u, kSc1));
 #pragma unroll
-      for (int j = 0; j < D / 8; ++j)
+      for (int j = 0; j < D / 16; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[j >> 2][(j & 3) * 4 + e] += x[j][e] * wi;
+        for (int e = 0; e < 8; ++e) {
+          const uint16_t bits = uint16_t(x[j][e >> 1] >> ((e & 1) * 16));
+          acc[j >> 1][(j & 1) * 8 + e] += c448 * float(__builtin_bit_cast(_Float16, bits));
+        }
     }
   }
   // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----

@@ -45,6 +45,10 @@ def lib():
         L.or_e4m3.argtypes = [_f]
         L.or_e4m3_to_f32.restype = _f
         L.or_e4m3_to_f32.argtypes = [ctypes.c_uint8]
+        L.or_f32_to_f16.restype = ctypes.c_uint16
+        L.or_f32_to_f16.argtypes = [_f]
+        L.or_f16_to_f32.restype = _f
+        L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.or_attention_f64.restype = None
         L.or_attention_f64.argtypes = [_p, _p, _p, _i, _i, _i, _i, _i, _f, _i, _i, _i64, _i64,
                                        _p, _p, _i, _p, _i]
@@ -91,6 +95,15 @@ def bf16_to_f32(h: np.ndarray) -> np.ndarray:
 
 def e4m3(x: float) -> int:
     return int(lib().or_e4m3(float(x)))
+
+
+def f16(x: float) -> int:
+    """IEEE binary16 bits of x, round to nearest even (the split partials' format)."""
+    return int(lib().or_f32_to_f16(float(x)))
+
+
+def f16_to_f32(h: int) -> float:
+    return float(lib().or_f16_to_f32(int(h)))
 
 
 def e4m3_to_f32(c: int) -> float:

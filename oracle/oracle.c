@@ -23,6 +23,8 @@
  *    rot = 0 and no norm is the identity, half mode = interleaved mode on
  *    permuted channels) and the butterfly order checked against a direct
  *    restatement of the reference's shuffle pattern.
+ *  - or_f32_to_f16 / or_f16_to_f32: pinned against numpy's IEEE float16 cast
+ *    (ties to even, subnormals, overflow) on hand cases and random values.
  *  - or_sage_emulate: pinned by its limit: with exact (unquantized) P/V it must
  *    equal or_attention_f64 to fp32 accuracy, and by the reference gate
  *    (rel-RMS < 4 % vs exact attention, tests/attention_fp8_test.cpp:65).
@@ -102,6 +104,47 @@ float or_e4m3_to_f32(uint8_t c) {
   if (e == 0) v = ldexpf((float)m, -9);
   else v = ldexpf(1.0f + m / 8.0f, e - 7);
   return s ? -v : v;
+}
+
+/* IEEE binary16 of a float, round to nearest even (overflow -> inf, subnormals kept);
+ * the build's split partials are stored in this format. Pinned in tests/test_oracle.py
+ * against numpy's float16 conversion and hand cases. */
+uint16_t or_f32_to_f16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const int e = (int)((u >> 23) & 0xff);
+  uint32_t mant = u & 0x7fffffu;
+  if (e == 0xff) return (uint16_t)(sign | 0x7c00u | (mant ? 0x200u : 0u));
+  const int exp = e - 127 + 15;
+  if (exp >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (exp <= 0) {
+    if (exp < -10) return sign;
+    mant |= 0x800000u;
+    const int shift = 14 - exp;
+    uint32_t half = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u), halfway = 1u << (shift - 1);
+    if (rem > halfway || (rem == halfway && (half & 1u))) ++half;
+    return (uint16_t)(sign | half);
+  }
+  uint32_t half = ((uint32_t)exp << 10) | (mant >> 13);
+  const uint32_t rem = mant & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (half & 1u))) ++half;  /* a carry may reach inf */
+  return (uint16_t)(sign | half);
+}
+
+float or_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const int e = (h >> 10) & 0x1f;
+  const uint32_t m = h & 0x3ffu;
+  float f;
+  if (e == 0) {
+    f = (float)m * 5.9604644775390625e-8f; /* 2^-24 */
+    return sign ? -f : f;
+  }
+  uint32_t u = e == 31 ? (sign | 0x7f800000u | (m << 13)) : (sign | ((uint32_t)(e - 15 + 127) << 23) | (m << 13));
+  memcpy(&f, &u, 4);
+  return f;
 }
 
 /* ---------- exact attention (double) ----------
@@ -320,8 +363,9 @@ static void or_sage_range(const int8_t* qr, float qscale, const int8_t* ki, cons
  * grid (units = (head, split_qt-query tile), unit index head * ceil(Sq/split_qt) +
  * row/split_qt). Units
  * at or past split_full run as split_parts ranges of key tiles, [j*nt/P, (j+1)*nt/P),
- * each with its own m, l, acc, merged as M = max m_j, w_j = 2^(m_j - M),
- * l = sum l_j w_j, acc = sum acc_j w_j in part order. split_parts <= 1: no split. */
+ * each with its own m, l, acc; a part keeps o_j = fp16(acc_j / (448 l_j)); merged as
+ * M = max m_j, w_j = 2^(m_j - M), c_j = l_j w_j, l = sum c_j, acc = sum (448 c_j) o_j
+ * in part order. split_parts <= 1: no split. */
 void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, const float* qs,
                      const float* ks, const float* vamax, int Sq, int Skv, int Hq, int Hkv, int D,
                      int64_t sq_pad, int64_t skv_pad, const uint8_t* kv_valid, const int* rows,
@@ -358,13 +402,20 @@ void or_sage_emulate(const int8_t* qi, const int8_t* ki, const uint8_t* vt, cons
     if (parts == 1) {
       memcpy(acc, pa, sizeof(float) * D);
     } else {
+      /* each part stores o_j = fp16(acc_j * (1 / (448 l_j))) (0 when l_j = 0) */
+      for (int j = 0; j < parts; ++j) {
+        const float inv = pl[j] > 0.f ? 1.f / (448.f * pl[j]) : 0.f;
+        for (int d = 0; d < D; ++d) pa[(size_t)j * D + d] = or_f16_to_f32(or_f32_to_f16(pa[(size_t)j * D + d] * inv));
+      }
       float mm = -INFINITY;
       for (int j = 0; j < parts; ++j) mm = fmaxf(mm, pm[j]);
       l = 0.f;
       for (int j = 0; j < parts; ++j) {
         const float w = mm == -INFINITY ? 0.f : (float)exp2((double)(pm[j] - mm));
-        l += pl[j] * w;
-        for (int d = 0; d < D; ++d) acc[d] += pa[(size_t)j * D + d] * w;
+        const float c = pl[j] * w;
+        l += c;
+        const float c448 = 448.f * c;
+        for (int d = 0; d < D; ++d) acc[d] += c448 * pa[(size_t)j * D + d];
       }
     }
     float* o = out + ((int64_t)ri * Hq + head) * D;

@@ -87,13 +87,14 @@ def test_workspace_and_layout():
         assert L[name] % 256 == 0
     assert L["qi"] == 0 and L["ki"] == 24 * 4352 * 128 and L["vt"] == 2 * 24 * 4352 * 128
     assert flash_attn_fp8_workspace(p) == L["total"]
-    # config 2: ~40 MB, plus one fp32 partial (acc, m, l per lane) per split work-group;
+    # config 2: ~40 MB, plus one partial (fp16 normalised output, fp32 m, l per lane)
+    # per split work-group;
     # the layout is a pure function of the shape (no device here): the pipelined kernel's
     # 128-query units, 816 on 512 work-group slots, the last 304 in three key ranges
     nw = L["split_qt"] // 32
     assert L["split_qt"] == 128 and L["split_units"] == 304 and L["split_parts"] == 3
-    assert L["total"] < 45e6 + 4 * (nw * 4224) * L["split_units"] * L["split_parts"]
-    assert L["cnt"] - L["split"] >= 4 * (nw * 4224) * L["split_units"] * L["split_parts"]
+    assert L["total"] < 45e6 + 4 * (nw * 2176) * L["split_units"] * L["split_parts"]
+    assert L["cnt"] - L["split"] >= 4 * (nw * 2176) * L["split_units"] * L["split_parts"]
     p2 = AttnParams(Sq=1000, Skv=77, Hq=4, Hkv=2, D=128)
     L2 = sage_layout(p2)
     assert L2["sq_pad"] == 1024 and L2["skv_pad"] == 128
@@ -154,11 +155,11 @@ def test_fp8_ok_rejects_keys_past_32bit_offsets():
 def test_workspace_layout_d64():
     """D = 64 runs the 8-wave kernel (256-query units): config-2 shape at D = 64 has 408
     units on 256 slots, so its last 152 units are split; the partials are sized for
-    D = 64 (8 waves x (8 float4 of acc + m, l) x 64 lanes)."""
+    D = 64 (8 waves x (32 fp16 of output + fp32 m, l) x 64 lanes)."""
     p = AttnParams(Sq=4352, Skv=4352, Hq=24, Hkv=24, D=64)
     L = sage_layout(p)
     assert L["split_qt"] == 256 and L["split_units"] == 152 and L["split_parts"] > 1
     assert L["ki"] == 24 * 4352 * 64 and L["vt"] == 2 * 24 * 4352 * 64
-    per_wg = 4 * (8 * 8 * 64 * 4 + 8 * 64 * 2)
+    per_wg = 4 * (8 * 4 * 64 * 4 + 8 * 64 * 2)
     assert L["cnt"] - L["split"] >= per_wg * L["split_units"] * L["split_parts"]
     assert L["cnt"] - L["split"] < per_wg * L["split_units"] * L["split_parts"] + 256
