@@ -3,8 +3,10 @@
 // Mirrors src/kernels/blockscale.h:12-37 of the reference (QMode, QMat, qmode_name,
 // parse_qmode, qmode_supported, qdata_bytes, qscale_bytes, quantize_blockscaled,
 // gemm_blockscaled: same names and argument order; cudaStream_t becomes hipStream_t,
-// and gemm_blockscaled takes the stream where the reference takes its Ctx, whose
-// cuBLASLt handle and workspace this kernel does not need). Errors surface as
+// and gemm_blockscaled takes either the stream or, as the reference (blockscale.h:34),
+// the caller's context: any object with a `stream` member convertible to hipStream_t,
+// so `gemm_blockscaled(ctx, ...)` call sites compile unchanged; the kernel needs no
+// cuBLASLt handle or workspace and runs on the current device). Errors surface as
 // std::runtime_error, as the reference's MX_CHECK does.
 #pragma once
 
@@ -14,6 +16,8 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <type_traits>
+#include <utility>
 
 #include "miroxen_attn.h"
 
@@ -59,6 +63,13 @@ inline void quantize_blockscaled(QMode m, const __hip_bfloat16* x, int64_t ldx, 
 inline void gemm_blockscaled(hipStream_t s, QMode m, const QMat& W, const QMat& X, __hip_bfloat16* Y, int64_t ldy,
                              int64_t M, int64_t N, int64_t K, float beta = 0.f) {
   detail::bs_check(mx_gemm_blockscaled(int(m), W.q, W.sf, X.q, X.sf, Y, ldy, M, N, K, beta, s));
+}
+
+// The reference's signature (src/kernels/blockscale.h:34-35): the context's stream.
+template <class Ctx, class = std::enable_if_t<std::is_convertible_v<decltype(std::declval<Ctx&>().stream), hipStream_t>>>
+inline void gemm_blockscaled(Ctx& c, QMode m, const QMat& W, const QMat& X, __hip_bfloat16* Y, int64_t ldy,
+                             int64_t M, int64_t N, int64_t K, float beta = 0.f) {
+  gemm_blockscaled(static_cast<hipStream_t>(c.stream), m, W, X, Y, ldy, M, N, K, beta);
 }
 
 }  // namespace mx

@@ -47,5 +47,23 @@ def build(verbose: bool = False, out: str = LIB, defines=()) -> str:
     return out
 
 
+CPP_CALLER_SRC = os.path.join(ROOT, "tests", "cpp", "attn_caller.cpp")
+CPP_CALLER = os.path.join(ROOT, "tests", "cpp", "_build", "attn_caller")
+
+
+def build_cpp_caller(verbose: bool = False) -> str:
+    """The C++ drop-in-header caller run by tests/test_gpu_cpp_caller.py (host code
+    linked against libmiroxen_attn.so; built here so GPU runs need no compiler)."""
+    os.makedirs(os.path.dirname(CPP_CALLER), exist_ok=True)
+    cmd = [hipcc(), "-std=c++17", "-O1", "-I", os.path.join(ROOT, "include"), CPP_CALLER_SRC, "-L", LIBDIR,
+           "-lmiroxen_attn", "-Wl,-rpath,$ORIGIN/../../../miroxen_amd/lib", "-o", CPP_CALLER]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stderr}")
+    return CPP_CALLER
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))

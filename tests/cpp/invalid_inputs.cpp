@@ -76,11 +76,17 @@ int main() {
   bs_ok += throws([&] { quantize_blockscaled(QMode::BF16, hb, 64, 4, 64, qm, nullptr); });
   bs_ok += throws([&] { gemm_blockscaled(nullptr, QMode::MXFP8, qm, qm, hb, 64, 4, 64, 64, 0.5f); });  // beta
   bs_ok += throws([&] { gemm_blockscaled(nullptr, QMode::NVFP4, qm, qm, hb, 64, 4, 64, 64); });
+  // the reference's call form: a context object carrying the stream (src/kernels/blockscale.h:34)
+  struct RefCtx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+  } ctx;
+  bs_ok += throws([&] { gemm_blockscaled(ctx, QMode::MXFP8, qm, qm, hb, 64, 4, 64, 64, 0.5f); });  // beta
   // the workspace query is pure host arithmetic
   AttnParams c2;
   c2.Sq = 4352; c2.Skv = 4352; c2.Hq = 24; c2.Hkv = 24; c2.D = 128;
   const size_t ws = flash_attn_fp8_workspace(c2);
-  std::printf("invalid input checks: %d rejected; head_norm_rope %d rejected; blockscale %d/9 ok; "
+  std::printf("invalid input checks: %d rejected; head_norm_rope %d rejected; blockscale %d/10 ok; "
               "config-2 workspace %zu bytes\n", rejected, nr_rejected, bs_ok, ws);
-  return rejected == 23 && nr_rejected == 1 && bs_ok == 9 && ws > 0 ? 0 : 1;
+  return rejected == 23 && nr_rejected == 1 && bs_ok == 10 && ws > 0 ? 0 : 1;
 }

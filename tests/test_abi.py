@@ -115,7 +115,7 @@ def test_cpp_dropin_header_rejects_invalid_inputs(tmp_path):
     subprocess.run(cmd, check=True, capture_output=True)
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert "23 rejected" in r.stdout and "blockscale 9/9 ok" in r.stdout
+    assert "23 rejected" in r.stdout and "blockscale 10/10 ok" in r.stdout
 
 
 @pytest.mark.parametrize("bad", [dict(D=7), dict(D=258), dict(rot=130), dict(rot=3), dict(mode=3),
