@@ -109,7 +109,8 @@ typedef struct mx_sage_layout {
   size_t qi, ki, vt, qs, ks, km, va, part, split, cnt, total;
   int split_units, split_parts;
   int split_qt; /* query rows per grid unit of the attention kernel (128 or 256) */
-  size_t tab;   /* [Hkv][skv_pad/64 + 1] 16-byte tile entries: liveness bits, K scale */
+  size_t tab;   /* [Hkv][skv_pad/64 + 1] 16-byte tile entries: liveness bits, K scale (negated
+                   when some key of the tile is dead) */
 } mx_sage_layout;
 int mx_sage_layout_of(const mx_attn_params* p, mx_sage_layout* out);
 

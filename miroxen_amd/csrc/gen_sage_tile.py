@@ -80,6 +80,7 @@ V_T0, V_T1, V_IM, V_LW = 224, 227, 226, 227
 TAB = (228, 232)
 V_LK, V_LV, V_U0 = 236, 237, 238
 V_LK2 = 231            # per-lane offset of the second K op (rows 32..63: 16-byte halves swapped)
+V_LV2 = 235            # per-lane offset of the second V^T op (16 channel rows further)
 ALPHA = (239, 225)     # rescale factor of the tiles of parity 0 / 1
 
 KTILE = 8192          # bytes per K or V^T tile slot
@@ -242,7 +243,7 @@ def mid_ops(par_next: int) -> list[str]:
     tab = TAB[par_next]
     u0, t0, t1, al = v(V_U0), v(V_T0), v(V_T1), v(ALPHA[par_next])
     return [
-        f"v_mul_f32 {v(V_SC)}, {v(V_QS)}, {v(tab + 2)}",
+        f"v_mul_f32 {v(V_SC)}, {v(V_QS)}, |{v(tab + 2)}|",                 # |ks|: the sign flags dead keys
         f"v_max_f32 {v(V_SC)}, {f32(1e-30)}, {v(V_SC)}",
         f"v_mul_f32 {u0}, {f32(12582912.0)}, {v(V_SC)}",                     # c2
         f"v_fma_f32 {t0}, {v(V_IM)}, {v(V_SC)}, -{u0}",                        # tmax
@@ -267,10 +268,22 @@ def l_rescale(par_next: int) -> str:
     return f"v_mul_f32 {v(V_L)}, {v(V_L)}, {v(ALPHA[par_next])}"
 
 
-def iteration(k: int) -> list[str]:
-    """Body of an iteration whose tile t satisfies t % 4 == k (SGPR %[t] holds t).
-    On entry v222 / v223 hold sc / nm of tile t and ALPHA[t % 2] / pend[t % 2] its
-    rescale factor; on exit the same for tile t+1."""
+# DMA variants of an iteration (tile t, last = the unit's last tile):
+#   "A": t + 4 <= last, DMAs K(t+4) and V(t+2) (4 ops);
+#   "B": t + 2 <= last < t + 4, DMAs V(t+2) only (2 ops);
+#   "C": last < t + 2, no DMA.
+# Tiles past the last are never loaded (their slots keep older, finite bytes: K is
+# int8, and V slots past the last are never read), so no load is in flight when the
+# unit ends. Each body ends by waiting until at most its own DMA ops are in flight,
+# i.e. for the ops of the previous iteration (the wait for iteration t-2's tiles at
+# the top of iteration t).
+NOPS = {"A": 4, "B": 2, "C": 0}
+
+
+def iteration(k: int, var: str) -> list[str]:
+    """Body of an iteration whose tile t satisfies t % 4 == k (SGPR %[t] holds t), DMA
+    variant `var`. On entry v222 / v223 hold sc / nm of tile t and ALPHA[t % 2] /
+    pend[t % 2] its rescale factor; on exit the same for tile t+1."""
     L: list[str] = []
     b = Block(L)
     par, nxt = k & 1, (k & 1) ^ 1
@@ -280,14 +293,14 @@ def iteration(k: int) -> list[str]:
     vs_prev = (k + 3) % 4   # V slot of tile t-1
     vs_cur = k              # V slot of tile t
     tab_next = TAB[nxt]
-    b.emit(f"sage_it{k}_%=:")
-    # 1. DMA of iteration t-2 landed; barrier: the slots of K(t) and V(t-2) are free
-    b.emit("s_waitcnt vmcnt(4)")
+    b.emit(f"sage_{var}{k}_%=:")
+    # 1. the barrier: every wave's DMA of iteration t-2 landed (each waited at the end
+    #    of iteration t-1), and the slots of K(t) and V(t-2) are free
     b.emit("s_barrier")
-    # table entry of tile t+1 (liveness for the max of S(t+1), K scale for its exponent)
-    b.emit("s_lshl_b32 %[s0], %[t], 4")
-    b.emit("s_add_u32 %[s0], %[s0], %[tab1]")  # tab1 = LDS address of the table + 16
-    b.emit(f"v_mov_b32 {v(V_U0)}, %[s0]")
+    # table entry of tile t+1 (liveness bits for the max of S(t+1), K scale for its
+    # exponent, its sign set when some key is dead); %[tabp] = its LDS address
+    b.emit(f"v_mov_b32 {v(V_U0)}, %[tabp]")
+    b.emit("s_add_u32 %[tabp], %[tabp], 16")
     b.read("TAB", tab_next, V_U0, 0, dwords=3)
     # 2. the softmax stream of S(t) with all twelve MFMAs of the iteration spread through
     #    it (one every seven stream instructions): the score MFMAs of S(t+1) first (their
@@ -313,21 +326,27 @@ def iteration(k: int) -> list[str]:
     # every ~20 stream instructions (a burst of them right after the barrier makes the
     # work-group's waves queue behind each other): the two K ops fill rows 0..31 and
     # 32..63 of d-chunk w (the second 4096 bytes further in memory, 1 KB further in LDS,
-    # 16-byte halves swapped: its own per-lane offset v231), the two V^T ops channel
-    # rows 32w..32w+15 and +16 (the second %[vstep] bytes further)
+    # 16-byte halves swapped: per-lane offset v231), the two V^T ops channel rows
+    # 32w..32w+15 and +16 (per-lane offsets v237, v235). %[kso] / %[vso] hold the
+    # scalar offsets of this iteration's tiles; M0 (the LDS destination) is written one
+    # stream instruction before the load that reads it.
     def dma_k(q):
-        return ["s_add_u32 %[s0], %[t], 4", "s_min_i32 %[s0], %[s0], %[last]", "s_lshl_b32 %[s0], %[s0], 13",
-                "s_add_u32 %[s0], %[s0], %[ksoff]"] + (["s_add_u32 %[s0], %[s0], 4096"] if q else []) + [
-                f"s_add_u32 m0, %[kdm0], {k * KTILE + q * 1024}", "s_nop 0",
-                f"buffer_load_dwordx4 {v(V_LK2 if q else V_LK)}, %[rk], %[s0] offen lds"]
+        return ([f"s_add_u32 m0, %[kdm0], {k * KTILE + q * 1024}"],
+                [f"buffer_load_dwordx4 {v(V_LK2 if q else V_LK)}, %[rk], %[kso] offen lds"])
 
     def dma_v(q):
-        return ["s_add_u32 %[s0], %[t], 2", "s_min_i32 %[s0], %[s0], %[last]", "s_lshl_b32 %[s0], %[s0], 6",
-                "s_add_u32 %[s0], %[s0], %[vsoff]"] + (["s_add_u32 %[s0], %[s0], %[vstep]"] if q else []) + [
-                f"s_add_u32 m0, %[vdm0], {ks2 * KTILE + q * 1024}", "s_nop 0",
-                f"buffer_load_dwordx4 {v(V_LV)}, %[rv], %[s0] offen lds"]
+        return ([f"s_add_u32 m0, %[vdm0], {ks2 * KTILE + q * 1024}"],
+                [f"buffer_load_dwordx4 {v(V_LV2 if q else V_LV)}, %[rv], %[vso] offen lds"])
 
-    dma_at = {6: dma_k(0), 27: dma_v(0), 48: dma_k(1), 69: dma_v(1)}
+    dma_at = {}
+    if var == "A":
+        for at, (m0, ld) in ((6, dma_k(0)), (48, dma_k(1))):
+            dma_at.setdefault(at, []).extend(m0)
+            dma_at.setdefault(at + 1, []).extend(ld)
+    if var in ("A", "B"):
+        for at, (m0, ld) in ((27, dma_v(0)), (69, dma_v(1))):
+            dma_at.setdefault(at, []).extend(m0)
+            dma_at.setdefault(at + 1, []).extend(ld)
 
     def do_read(r):
         tag, kind, kk, x = r
@@ -345,6 +364,7 @@ def iteration(k: int) -> list[str]:
     # from `mx_at` (the first 8 max ops read key block 0 of S(t+1), the rest key block 1);
     # the update's writes of sc / nm / l come after the stream's last use of them.
     mx_at = max(s_last[0] + 20, pos[-1] + 2)
+    flag_at = mx_at - 8  # the table entry's K-scale word -> SGPR, well before the branch
     n = kq = 0
     issue: dict[int, list] = {}
     for ins in valu[:mx_at]:
@@ -354,6 +374,9 @@ def iteration(k: int) -> list[str]:
             do_read(r)
         for x in dma_at.pop(n, []):
             b.emit(x)
+        if n == flag_at:
+            b.wait_for("TAB")
+            b.emit(f"v_readfirstlane_b32 %[s0], {v(tab_next + 2)}")
         if kq < len(mf) and n == pos[kq]:
             text, needs, after = mf[kq]
             b.wait_for(*needs)
@@ -362,19 +385,16 @@ def iteration(k: int) -> list[str]:
             kq += 1
     assert kq == len(mf) and not issue and not dma_at, (kq, issue, dma_at)
     tail = valu[mx_at:]
-    # liveness of tile t+1: all live -> FULL tail, else PART tail
-    b.wait_for("TAB")
-    b.emit(f"v_readfirstlane_b32 %[s0], {v(tab_next)}")
-    b.emit(f"v_readfirstlane_b32 %[s1], {v(tab_next + 1)}")
-    b.emit("s_nop 4")
-    b.emit("s_and_b32 %[s0], %[s0], %[s1]")
-    # the last iteration has no tile t+1: its update must leave m, l and alpha alone, so
-    # it takes the PART path with every key dead (row max -inf: m does not move)
-    b.emit("s_add_u32 %[s2], %[t], 1")
-    b.emit("s_cmp_lt_i32 %[s2], %[nt]")
-    b.emit("s_cselect_b32 %[s0], %[s0], 0")
-    b.emit("s_cmp_eq_u32 %[s0], -1")
-    b.emit(f"s_cbranch_scc0 sage_part{k}_%=")
+    # tile t+1 with a dead key (sign of its K-scale word) -> PART tail, else FULL tail.
+    # Variant C may run the unit's last iteration, which has no tile t+1: its update
+    # must leave m, l and alpha alone, so it takes the PART path with every key dead
+    # (row max -inf: m does not move)
+    if var == "C":
+        b.emit("s_add_u32 %[s2], %[t], 1")
+        b.emit("s_cmp_lt_i32 %[s2], %[nt]")
+        b.emit("s_cselect_b32 %[s0], %[s0], -1")
+    b.emit("s_cmp_lt_i32 %[s0], 0")
+    b.emit(f"s_cbranch_scc1 sage_part{var}{k}_%=")
     # FULL: the max ops go one after each stream op; the update ops follow the max tree
     # and the stream's last use of sc / nm (fma) and write of l (the tile's row sum)
     xs, ys = max_tree(nxt), mid_ops(nxt)
@@ -399,35 +419,49 @@ def iteration(k: int) -> list[str]:
     first1 = min(i for i, x in enumerate(stream) if srcs(x) & kb1)
     assert first0 + 1 - s_last[0] >= 20 and first1 + 1 - s_last[1] >= 20, (first0, first1, pos)
     L.extend(full_tail)
-    b.emit(f"s_branch sage_join{k}_%=")
-    b.emit(f"sage_part{k}_%=:")
+    b.emit(f"s_branch sage_join{var}{k}_%=")
+    b.emit(f"sage_part{var}{k}_%=:")
     L.extend(tail)
     assert len(valu) - s_last[1] >= 20
     # this lane's word: keys 32h .. 32h+31 (%[hmask]: lanes 32..63)
     b.emit(f"v_cndmask_b32 {v(V_LW)}, {v(tab_next)}, {v(tab_next + 1)}, %[hmask]")
-    b.emit("s_cmp_lt_i32 %[s2], %[nt]")
-    b.emit(f"s_cbranch_scc1 sage_live{k}_%=")
-    b.emit(f"v_mov_b32 {v(V_LW)}, 0")
-    b.emit(f"sage_live{k}_%=:")
+    if var == "C":
+        b.emit("s_cmp_lt_i32 %[s2], %[nt]")
+        b.emit(f"s_cbranch_scc1 sage_live{var}{k}_%=")
+        b.emit(f"v_mov_b32 {v(V_LW)}, 0")
+        b.emit(f"sage_live{var}{k}_%=:")
     L.extend(mask_ops(nxt))
     L.extend(max_tree(nxt))
     L.extend(mid_ops(nxt))
     L.append(l_rescale(nxt))
-    b.emit(f"sage_join{k}_%=:")
+    b.emit(f"sage_join{var}{k}_%=:")
     b.drain()
     # 4. rescale of the accumulators by alpha(t) when the running max moved at tile t
     #    (P(t-1) V(t-1), issued in blocks A and B, completed long before)
     b.emit(f"s_cmp_eq_u64 %[pend{par}], 0")
-    b.emit(f"s_cbranch_scc1 sage_norescale{k}_%=")
+    b.emit(f"s_cbranch_scc1 sage_norescale{var}{k}_%=")
     for r in range(64):
         b.emit(f"v_mul_f32 {v(ACC + r)}, {v(ALPHA[par])}, {v(ACC + r)}")
-    b.emit(f"sage_norescale{k}_%=:")
-    # next tile
+    b.emit(f"sage_norescale{var}{k}_%=:")
+    # this iteration's DMA ops may stay in flight; the previous iteration's have landed
+    b.emit(f"s_waitcnt vmcnt({NOPS[var]})")
+    # next tile: advance the scalar DMA offsets, then the variant of tile t+1
     b.emit("s_add_u32 %[t], %[t], 1")
-    b.emit("s_cmp_ge_i32 %[t], %[nt]")
-    b.emit(f"s_cbranch_scc1 sage_drain{k}_%=")
+    k1 = (k + 1) % 4
+    if var == "A":
+        b.emit(f"s_add_u32 %[kso], %[kso], {KTILE}")
+        b.emit("s_add_u32 %[vso], %[vso], 64")
+        b.emit("s_cmp_ge_i32 %[t], %[klim]")
+        b.emit(f"s_cbranch_scc1 sage_B{k1}_%=")
+    elif var == "B":
+        b.emit("s_add_u32 %[vso], %[vso], 64")
+        b.emit("s_cmp_ge_i32 %[t], %[vlim]")
+        b.emit(f"s_cbranch_scc1 sage_C{k1}_%=")
+    else:
+        b.emit("s_cmp_ge_i32 %[t], %[nt]")
+        b.emit(f"s_cbranch_scc1 sage_drain{k}_%=")
     if k == 3:
-        b.emit("s_branch sage_it0_%=")
+        b.emit(f"s_branch sage_{var}0_%=")
     return L
 
 
@@ -452,11 +486,20 @@ def drain(k: int) -> list[str]:
 
 
 def loop() -> list[str]:
-    L = ["s_mov_b32 %[m0save], m0", "s_and_b32 %[s0], %[t], 3"]
-    for k in (1, 2, 3):
-        L += [f"s_cmp_eq_u32 %[s0], {k}", f"s_cbranch_scc1 sage_it{k}_%="]
-    for k in range(4):
-        L += iteration(k)
+    """Entry: the variant of tile t (%[klim] = last - 3, %[vlim] = last - 1), then its
+    slot phase t % 4."""
+    L = ["s_mov_b32 %[m0save], m0", "s_and_b32 %[s0], %[t], 3",
+         "s_cmp_ge_i32 %[t], %[vlim]", "s_cbranch_scc1 sage_entryC_%=",
+         "s_cmp_ge_i32 %[t], %[klim]", "s_cbranch_scc1 sage_entryB_%="]
+    for var in "ABC":
+        if var != "A":
+            L.append(f"sage_entry{var}_%=:")
+        for k in (1, 2, 3):
+            L += [f"s_cmp_eq_u32 %[s0], {k}", f"s_cbranch_scc1 sage_{var}{k}_%="]
+        L.append(f"s_branch sage_{var}0_%=")
+    for var in "ABC":
+        for k in range(4):
+            L += iteration(k, var)
     for k in range(4):
         L += drain(k)
     L += ["sage_end_%=:", "s_mov_b32 m0, %[m0save]"]

@@ -314,14 +314,16 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
     *reinterpret_cast<u32x2*>(ki + (int64_t(h) * skv_pad + k0 + r0 + RPP * i) * D + c) = quant8(x[i], inv);
   if (tid == 0) ks[int64_t(h) * (skv_pad / kKvPad) + blockIdx.x] = am / 127.f * 1.f;
   // tile table of the attention kernel: liveness bits of the tile's 64 keys (mask and
-  // tail) and its K scale
+  // tail) and its K scale, negated when some key is dead (the kernel's loop branches on
+  // that sign and uses the magnitude)
   if (tid < 64) {
     const int64_t key = k0 + tid;
     const bool live = key < p.Skv && (!p.kv_valid || p.kv_valid[key]);
     const uint64_t bits = __ballot(live);
     if (tid == 0)
       tab[int64_t(h) * (skv_pad / kKvPad + 1) + blockIdx.x] =
-          u32x4{uint32_t(bits), uint32_t(bits >> 32), __float_as_uint(am / 127.f * 1.f), 0u};
+          u32x4{uint32_t(bits), uint32_t(bits >> 32), __float_as_uint(bits == ~0ull ? am / 127.f : -(am / 127.f)),
+                0u};
   }
   // V^T rows: channel d, 64 keys = 4 x 16 bytes
   for (int i = tid; i < D * (kKvPad / 16); i += 256) {
@@ -802,7 +804,7 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int kr = lane >> 1, vr = lane >> 2;
   const uint32_t lk0 = uint32_t(kr * D + ((lane & 1) << 4));
-  const uint32_t lk1 = uint32_t((32 + kr) * D + (((lane & 1) ^ 1) << 4)) - 4096u;  // soffset adds 4096
+  const uint32_t lk1 = uint32_t((32 + kr) * D + (((lane & 1) ^ 1) << 4));
   const uint32_t lv = uint32_t(vr) * uint32_t(skv_pad) + uint32_t(((lane & 3) ^ ((vr >> 2) & 3)) << 4);
   const uint32_t ksoff = uint32_t(wave_u * 32), vsoff = uint32_t(2 * wave_u * 16) * uint32_t(skv_pad);
   const uint32_t vstep = uint32_t(16) * uint32_t(skv_pad);
@@ -812,7 +814,7 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
     const uint32_t so = ksoff + uint32_t((tile < last ? tile : last) * (KT * D));
     unsigned char* d = kring + (slot & 3) * KTILEB + 2 * wave_u * 1024;
     buf2lds16(rk_r, lk0, so, (MXA_LDS void*)d);
-    buf2lds16(rk_r, lk1, so + 4096u, (MXA_LDS void*)(d + 1024));
+    buf2lds16(rk_r, lk1, so, (MXA_LDS void*)(d + 1024));
   };
   auto dma_v = [&](int tile, int slot) __attribute__((always_inline)) {
     const uint32_t so = vsoff + uint32_t((tile < last ? tile : last) * KT);
@@ -917,11 +919,12 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   const i32x4 tabi = __builtin_bit_cast(i32x4, tab0);
   i32x8 tabs = __builtin_shufflevector(tabi, tabi, 0, 1, 2, 3, 4, 5, 6, 7);
   tabs[3] = int(lk1);
+  tabs[7] = int(lv + vstep);  // the second V^T op's per-lane offset
   i32x16 pbuf = {};  // P buffers; P(tb - 1) = 0
   f32x16 acc0 = {}, acc1 = {}, acc2 = {}, acc3 = {};
   // running max, exponent offset and scale of tile tb (the loop computes them for the
   // next tile at the end of each iteration): m = tmax unless every key is dead
-  const float sc = fmaxf(qscale * __uint_as_float(tab0[2]), 1e-30f), c2 = 12582912.f * sc;
+  const float sc = fmaxf(qscale * fabsf(__uint_as_float(tab0[2])), 1e-30f), c2 = 12582912.f * sc;
   float m = __builtin_fmaf(__int_as_float(im), sc, -c2);  // -inf when every key of tile tb is dead
   float nm = (kLog2_448 - kSageHeadroom - fmaxf(m, -3.0e38f)) - c2;
   float l = 0.f, alpha0 = 1.f, alpha1 = 1.f;
@@ -929,7 +932,12 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   int t = tb;
   int s_0, s_1, s_2, m0save;  // scalar scratch of the loop (M0 is saved and restored)
   const uint32_t kdm0 = kring_l + uint32_t(2 * wave_u * 1024), vdm0 = vring_l + uint32_t(2 * wave_u * 1024);
-  const uint32_t tab1 = table_l + 16u;
+  // scalar state of the loop: the LDS address of tile t+1's table entry, the buffer
+  // offsets of K(t+4) and V^T(t+2) (this wave's ops), and the variant limits (tiles up
+  // to klim - 1 DMA K(t+4) and V(t+2), up to vlim - 1 only V(t+2))
+  uint32_t tabp = table_l + uint32_t(tb + 1) * 16u;
+  uint32_t kso = ksoff + uint32_t(tb + 4) * uint32_t(KT * D), vso = vsoff + uint32_t(tb + 2) * uint32_t(KT);
+  const int klim = last - 3, vlim = last - 1;
   const uint64_t hmask = 0xffffffff00000000ull;
   float sc_v = sc;
   const uint32_t kb_l = kring_l + kbase, vb0_l = vring_l + vbase0, vb1_l = vring_l + vbase1;
@@ -946,11 +954,11 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
                  "+{v[152:167]}"(vtr), "+{v219}"(m), "+{v220}"(l), "+{v226}"(im), "+{v[228:235]}"(tabs),
                  "+{v222}"(sc_v), "+{v223}"(nm), "+{v239}"(alpha0), "+{v225}"(alpha1), [t] "+s"(t),
                  [s0] "=&s"(s_0), [s1] "=&s"(s_1), [s2] "=&s"(s_2), [pend0] "+s"(pend0), [pend1] "+s"(pend1),
-                 [m0save] "=&s"(m0save)
+                 [m0save] "=&s"(m0save), [tabp] "+s"(tabp), [kso] "+s"(kso), [vso] "+s"(vso)
                : "{v[168:183]}"(q16), "{v[184:199]}"(bias), "{v216}"(kb_l), "{v217}"(vb0_l), "{v218}"(vb1_l),
-                 "{v221}"(qscale), "{v236}"(lk0), "{v237}"(lv), [nt] "s"(nt), [last] "s"(last), [ksoff] "s"(ksoff),
-                 [vsoff] "s"(vsoff), [vstep] "s"(vstep), [kdm0] "s"(kdm0), [vdm0] "s"(vdm0), [tab1] "s"(tab1),
-                 [rk] "s"(rk), [rv] "s"(rv), [hmask] "s"(hmask), [kdead] "s"(kDead)
+                 "{v221}"(qscale), "{v236}"(lk0), "{v237}"(lv), [nt] "s"(nt), [klim] "s"(klim), [vlim] "s"(vlim),
+                 [kdm0] "s"(kdm0), [vdm0] "s"(vdm0), [rk] "s"(rk), [rv] "s"(rv), [hmask] "s"(hmask),
+                 [kdead] "s"(kDead)
                : "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", "v211",
                  "v212", "v213", "v214", "v215", "v224", "v227", "v238", "vcc", "scc", "memory");
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
