@@ -499,8 +499,7 @@ __device__ __forceinline__ void sage_load_tile(const SageAddr<D>& a, int tk, int
 template <int NW, int D>
 __device__ __forceinline__ void sage_finish(f32x16 (&acc)[D / 32], float m, float l, int part, int su, const SageSplit& sp,
                                             int wave, int lane, int row, const mx_attn_params& p,
-                                            const float* __restrict__ va, int kvh, int head,
-                                            uint16_t* __restrict__ o) {
+                                            const float* __restrict__ vah, int head, uint16_t* __restrict__ o) {
   const int h = lane >> 5;
   if (part >= 0) {
     // Split unit: publish (o, m, l), then the last part to arrive merges all parts.
@@ -586,7 +585,6 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[D / 32], float m, floa
   }
   // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----
   if (row < p.Sq) {
-    const float* vah = va + kvh * D;
     const float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
     uint16_t* dst = o + int64_t(row) * p.o_stride + head * D + h * 4;
 #pragma unroll
@@ -742,7 +740,7 @@ sage_attn_gen(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, cons
   }
 
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
-  sage_finish<NW, D>(acc, m, l, part, su, sp, wave, lane, row, p, va, kvh, head, o);
+  sage_finish<NW, D>(acc, m, l, part, su, sp, wave, lane, row, p, va + kvh * D, head, o);
 }
 
 // ---------------- software-pipelined main kernel ----------------
@@ -778,6 +776,7 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   __shared__ __align__(16) unsigned char kring[4 * KTILEB];
   __shared__ __align__(16) unsigned char vring[4 * VTILEB];
   __shared__ __align__(16) u32x4 table[kPipeMaxTiles + 1];
+  __shared__ __align__(16) float vas[kPipeD];  // the head's V channel scales, for the epilogue
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 31, h = lane >> 5;
   const int ntq = (p.Sq + QT - 1) / QT;
   const int nkt = (p.Skv + KT - 1) / KT;
@@ -854,6 +853,7 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
       if (i < nkt) table[i] = e[j];
     }
     if (threadIdx.x == 0) table[nkt] = u32x4{~0u, ~0u, 0u, 0u};
+    if (threadIdx.x < D) vas[threadIdx.x] = va[kvh * D + threadIdx.x];
   }
   wait_vm_n<0>();
   __syncthreads();  // K(tb..tb+3), V(tb), V(tb+1) and the tile table are visible
@@ -964,7 +964,7 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
   f32x16 acc[4] = {acc0, acc1, acc2, acc3};
   l += other_half(l);  // the wave halves summed different keys of the same rows
-  sage_finish<NW, D>(acc, m, l, part, su, sp, wave, lane, row, p, va, kvh, head, o);
+  sage_finish<NW, D>(acc, m, l, part, su, sp, wave, lane, row, p, vas, head, o);
 }
 
 }  // namespace
