@@ -21,53 +21,26 @@
 //    prove an in-flight DMA never aliases the buffers being read and does not
 //    wait for it; waits are explicit, counted vmcnt. DMA ops are spread one per
 //    four MFMAs (a burst of them stalls the issuing waves for hundreds of cycles).
-//  * Two work-group shapes (selected at build time, MXA_BF16_KIND), both
-//    8 waves of 32 queries, two waves per SIMD:
-//     PP (9, default): ping-pong. The two waves of a SIMD run the same program
-//        one period apart, so one issues the tile's MFMAs while the other runs
-//        the softmax (VALU); measured ~5% faster than W8.
-//     W8 (8): lockstep, per tile S -> softmax -> P*V on every wave.
-//    Within an MFMA phase, sched_group_barrier keeps LDS operand reads a few
-//    MFMAs ahead of use.
+//  * Work-group: 8 waves of 32 queries, two waves per SIMD, ping-pong: the two
+//    waves of a SIMD run the same program one period apart, so one issues the
+//    tile's MFMAs while the other runs the softmax (VALU); measured ~5% faster
+//    than all waves in lockstep. Within an MFMA phase, sched_group_barrier keeps
+//    LDS operand reads a few MFMAs ahead of use (kKPrefetch / kVPrefetch).
 //  * Work-groups are remapped so one head's query tiles share an XCD (and its L2).
 #include <type_traits>
 #include <utility>
 
 #include "attn_common.hpp"
 
-#ifndef MXA_BF16_KIND
-#define MXA_BF16_KIND 9
-#endif
-#ifndef MXA_KPF
-#define MXA_KPF 3
-#endif
-#ifndef MXA_VPF
-#define MXA_VPF 2
-#endif
 
 namespace mxa {
 
-#ifdef MXA_CLOCK
-// Development hook (off in normal builds): per-work-group shader-clock and
-// real-time durations, written where mx_debug_timing points.
-__device__ uint64_t* g_timing = nullptr;
-extern "C" int mx_debug_timing(void* buf) {
-  return hipMemcpyToSymbol(HIP_SYMBOL(g_timing), &buf, sizeof(buf)) == hipSuccess ? 0 : -2;
-}
-#define MXA_CLOCK_BEGIN const uint64_t clk0_ = __builtin_amdgcn_s_memtime(), rt0_ = __builtin_amdgcn_s_memrealtime();
-#define MXA_CLOCK_END                                                               \
-  if (threadIdx.x == 0 && g_timing) {                                               \
-    g_timing[blockIdx.x * 2] = __builtin_amdgcn_s_memtime() - clk0_;                \
-    g_timing[blockIdx.x * 2 + 1] = __builtin_amdgcn_s_memrealtime() - rt0_;         \
-  }
-#else
-#define MXA_CLOCK_BEGIN
-#define MXA_CLOCK_END
-#endif
 
 namespace {
 
 constexpr int KT = 64;               // keys per tile
+constexpr int kKPrefetch = 3;        // K operand reads issued this many MFMAs ahead (scores)
+constexpr int kVPrefetch = 2;        // V operand reads issued this many MFMAs ahead (P V)
 
 // LDS tile layouts (16 KB each at D = 128, filled by DMA ops of 1 KB):
 //  K: [D/16 d-chunks of 16][64 rows][2 halves of 8 channels]; the 16-byte half is
@@ -316,7 +289,7 @@ __device__ __forceinline__ void rescale(QBlock<DH>& X) {
 // between the MFMAs, so no wave issues a burst of DMA ops at once.
 template <int NMF, int LD>
 __device__ __forceinline__ void sched_k() {
-  constexpr int PF = MXA_KPF < NMF ? MXA_KPF : NMF;
+  constexpr int PF = kKPrefetch < NMF ? kKPrefetch : NMF;
   __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
 #pragma unroll
   for (int i = 0; i < NMF; ++i) {
@@ -327,7 +300,7 @@ __device__ __forceinline__ void sched_k() {
 }
 template <int NMF, int LD>
 __device__ __forceinline__ void sched_v() {
-  constexpr int PF = MXA_VPF < NMF ? MXA_VPF : NMF;
+  constexpr int PF = kVPrefetch < NMF ? kVPrefetch : NMF;
   __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF, 0);
 #pragma unroll
   for (int i = 0; i < NMF; ++i) {
@@ -355,73 +328,6 @@ __device__ __forceinline__ void store_block(const QBlock<DH>& X, uint16_t* o, co
     }
 }
 
-// ---------------- W8: 8 waves x 32 queries, lockstep ----------------
-// Per tile S -> softmax -> P*V on every wave; the two waves of a SIMD overlap
-// only where their phases happen to drift apart. Two-stage K/V ring: tile t
-// lives in stage t % 2 and the loads of tile t + 1 (clamped to the last tile,
-// so the ops are unconditional and interleave with the MFMAs) go into the
-// stage tile t - 1 used.
-template <int DH, bool CAUSAL>
-__global__ void __launch_bounds__(512, 1)
-flash_bf16_w8(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-              uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign) {
-  using Dm = Dims<DH>;
-  constexpr int NW = 8, QT = NW * 32;
-  constexpr int OPS = (Dm::KOPS + NW - 1) / NW + (Dm::VOPS + NW - 1) / NW;  // DMA ops per wave per tile
-  __shared__ __align__(16) unsigned char st0[Dm::KTB + Dm::VTB];
-  __shared__ __align__(16) unsigned char st1[Dm::KTB + Dm::VTB];
-  __shared__ uint64_t live_tiles[kMaxLiveTiles];
-  MXA_CLOCK_BEGIN
-  const Lane ln(c);
-  const int wave = threadIdx.x >> 6;
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const int ntq = (p.Sq + QT - 1) / QT;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  // causal: query tiles with the most key tiles first
-  const int head = L / ntq, qtile = CAUSAL ? ntq - 1 - L % ntq : L % ntq;
-  const int kvh = head / (p.Hq / p.Hkv);
-  const int q0 = qtile * QT + wave * 32;
-  const int nt = tiles_needed<CAUSAL>(p, qtile * QT, QT);
-  const int64_t kvbase = int64_t(kvh) * DH;
-  const TileAddr ta = tile_addr<NW>(p, wave_u, ln.lane);
-
-  QBlock<DH> A;
-  qblock_init(A, q, p, q0, head, ln, qsign);
-  if (CAUSAL && nt == 0) {  // causal: no visible key for any query of the work-group -> 0
-    store_block(A, o, p, q0, head, ln);
-    return;
-  }
-  auto issue = [&](int t, unsigned char* dst) __attribute__((always_inline)) {
-    load_tile<NW, false, DH>(k, t, dst, p, kvbase, wave_u, ta);
-    load_tile<NW, true, DH>(v, t, dst + Dm::KTB, p, kvbase, wave_u, ta);
-  };
-  issue(0, st0);
-  build_live<NW, KT>(live_tiles, p, nt, wave, ln.lane);
-  __syncthreads();  // bitmaps visible (once, before the pipelined loop)
-
-  auto step = [&](int t, unsigned char* cur, unsigned char* nxt) __attribute__((always_inline)) {
-    wait_vm_n<0>();  // tile t landed
-    block_sync();    // ... for every wave, and tile t - 1's stage is free
-    const uint64_t live = tile_live<KT>(live_tiles, p, t);
-    issue(t + 1 < nt ? t + 1 : nt - 1, nxt);
-    scores(cur, A, ln);
-    sched_k<2 * Dm::NC, OPS>();
-    const bool diag = CAUSAL && int64_t(p.q_offset) + q0 - int64_t(t) * KT < KT - 1;  // wave-uniform
-    if (live != ~0ull || diag) mask_scores<CAUSAL>(A, live, diag ? causal_rel(p, q0 + ln.n, t) : KT - 1, ln);
-    softmax(A, ln);
-    rescale(A);
-    pv(cur + Dm::KTB, A, ln);
-    sched_v<4 * Dm::NB, 0>();
-  };
-  for (int t = 0; t < nt; t += 2) {
-    step(t, st0, st1);
-    if (t + 1 < nt) step(t + 1, st1, st0);
-  }
-  wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
-  store_block(A, o, p, q0, head, ln);
-  MXA_CLOCK_END
-}
-
 // ---------------- PP: 8 waves x 32 queries, ping-pong groups ----------------
 // Waves w and w + 4 share a SIMD. Group A (waves 0-3) and group B (waves 4-7)
 // run the same per-tile program offset by one period, so in every period one
@@ -446,7 +352,6 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
   __shared__ __align__(16) unsigned char vb0[Dm::VTB];
   __shared__ __align__(16) unsigned char vb1[Dm::VTB];
   __shared__ uint64_t live_tiles[kMaxLiveTiles];
-  MXA_CLOCK_BEGIN
   const Lane ln(c);
   const int wave = threadIdx.x >> 6;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -537,7 +442,6 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
   }
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
   store_block(A, o, p, q0, head, ln);
-  MXA_CLOCK_END
 }
 
 }  // namespace
@@ -549,7 +453,7 @@ hipError_t launch_flash_bf16(const uint16_t* q, const uint16_t* k, const uint16_
                              const mx_attn_params& p, hipStream_t s) {
   const float c = __builtin_fabsf(p.scale) * kLog2e;
   const uint32_t qsign = p.scale < 0.f ? 0x80008000u : 0u;
-  constexpr int QT = 256;  // both shapes cover 256 queries per work-group
+  constexpr int QT = 256;  // queries per work-group
   const int ntq = (p.Sq + QT - 1) / QT;
   const int64_t blocks = int64_t(ntq) * p.Hq;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
@@ -558,11 +462,7 @@ hipError_t launch_flash_bf16(const uint16_t* q, const uint16_t* k, const uint16_
   const bool cz = p.causal != 0;
   switch (p.D) {
     case 128:
-#if MXA_BF16_KIND == 8
-      cz ? go(flash_bf16_w8<128, true>) : go(flash_bf16_w8<128, false>);
-#else
       cz ? go(flash_bf16_pp<128, true>) : go(flash_bf16_pp<128, false>);
-#endif
       break;
     case 64: cz ? go(flash_bf16_pp<64, true>) : go(flash_bf16_pp<64, false>); break;
     case 72: cz ? go(flash_bf16_pp<72, true>) : go(flash_bf16_pp<72, false>); break;

@@ -3,8 +3,9 @@
 // (src/kernels/attention.cu:292-348): fp32 dot products, expf, online
 // max/sum over 128-key chunks, bf16 output, 0 when the row has no live key.
 // Extended with the key-padding mask. Besides attn_reference it is the general
-// path of flash_attn for the variants the MFMA kernel does not cover yet
-// (causal, D in {64,72}, unaligned strides).
+// path of flash_attn where the MFMA kernel's preconditions fail (token strides not a
+// multiple of 8 elements or operands not 16-byte aligned, masked Skv > 65536, K/V
+// beyond 32-bit buffer offsets).
 #include "attn_common.hpp"
 
 namespace mxa {
