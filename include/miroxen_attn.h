@@ -72,6 +72,12 @@ int mx_flash_attn_fp8_ok(const void* q, const void* k, const void* v, const void
 int mx_flash_attn_fp8(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
                       void* ws, void* stream);
 
+/* No counterpart in the reference (a diagnostic query): *mfma = 1 when mx_flash_attn
+ * runs the MFMA kernel for these arguments, 0 when it runs the general (naive) kernel.
+ * Validates like mx_flash_attn; launches nothing. */
+int mx_flash_attn_uses_mfma(const void* q, const void* k, const void* v, const void* o, const mx_attn_params* p,
+                            int* mfma);
+
 /* No counterpart in the reference. For callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc):
  * mx_flash_attn_fp8 with the workspace taken from a fixed library-owned device scratch

@@ -83,6 +83,16 @@ def flash_attn_fp8_supported(device: int) -> bool:
     return bool(out.value)
 
 
+def flash_attn_uses_mfma(q, k, v, o, p: AttnParams) -> bool:
+    """Whether flash_attn runs the MFMA kernel for these arguments (else the general
+    kernel); a diagnostic query with no counterpart in the reference."""
+    c = p.c()
+    res = ctypes.c_int(0)
+    _lib.check(_lib.load().mx_flash_attn_uses_mfma(_addr(q), _addr(k), _addr(v), _addr(o), ctypes.byref(c),
+                                                   ctypes.byref(res)))
+    return bool(res.value)
+
+
 def flash_attn_fp8_ok(q, k, v, o, p: AttnParams) -> bool:
     """Reference mx::flash_attn_fp8_ok (src/kernels/attention_fp8.cu:484-486)."""
     c = p.c()

@@ -103,9 +103,9 @@ bool device_is_gfx950(int device) {
 int fp8_ok(const void* q, const void* k, const void* v, const void* o, const mx_attn_params& p, bool* ok) {
   *ok = false;
   if (p.causal || (p.D != 128 && p.D != 64) || p.Sq <= 0 || p.Skv <= 0 || p.Hkv <= 0 || p.Hq <= 0 || p.Hq % p.Hkv) return MX_OK;
-  if (p.q_stride % 8 || p.kv_stride % 8 || p.o_stride % 2 || !aligned(q, 16) || !aligned(k, 16) ||
-      !aligned(v, 16) || !aligned(o, 4))
-    return MX_OK;
+  // bf16 operands at their natural 2-byte alignment, any token stride: gfx950 serves the
+  // kernels' 16-byte row loads and 4-byte stores at 2-byte granularity
+  if (!aligned(q, 2) || !aligned(k, 2) || !aligned(v, 2) || !aligned(o, 2)) return MX_OK;
   if (!(p.scale > 0.f) || p.Hq > 65535 || (p.kv_valid && p.Skv > kMaxMaskedSkv)) return MX_OK;
   const int64_t skv_pad = (int64_t(p.Skv) + mxa::kKvPad - 1) / mxa::kKvPad * mxa::kKvPad;
   if (skv_pad * p.D >= (int64_t(1) << 32)) return MX_OK;
@@ -116,9 +116,12 @@ int fp8_ok(const void* q, const void* k, const void* v, const void* o, const mx_
   return MX_OK;
 }
 
+// The MFMA kernel's preconditions. Token strides need not be multiples of 8 (the
+// reference's Aligned = false case, attention.cu:55-63, :383-389): the kernel's 16-byte
+// K/V tile loads (buffer -> LDS), Q loads and 4-byte O stores are served at 2-byte
+// granularity by gfx950's memory system, so one kernel covers both cases.
 bool fast_bf16_ok(const void* q, const void* k, const void* v, const void* o, const mx_attn_params& p) {
-  return p.q_stride % 8 == 0 && p.kv_stride % 8 == 0 && p.o_stride % 2 == 0 &&
-         aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 4) &&
+  return aligned(q, 2) && aligned(k, 2) && aligned(v, 2) && aligned(o, 2) &&
          (!p.kv_valid || p.Skv <= kMaxMaskedSkv) &&
          int64_t(p.Skv) * p.kv_stride * 2 < (int64_t(1) << 32);  // K/V tiles read through 32-bit buffer offsets
 }
@@ -171,6 +174,16 @@ int mx_flash_attn(const void* q, const void* k, const void* v, void* o, const mx
   auto oo = static_cast<uint16_t*>(o);
   if (fast_bf16_ok(q, k, v, o, a)) return hip_status(mxa::launch_flash_bf16(qq, kk, vv, oo, a, s), "flash_attn");
   return hip_status(mxa::launch_naive_attn(qq, kk, vv, oo, a, s), "flash_attn");
+}
+
+int mx_flash_attn_uses_mfma(const void* q, const void* k, const void* v, const void* o, const mx_attn_params* p,
+                            int* mfma) {
+  if (!mfma) return fail(MX_E_INVALID, "flash_attn_uses_mfma: null output");
+  mx_attn_params a;
+  int rc = validate(q, k, v, o, p, &a);
+  if (rc) return rc;
+  *mfma = fast_bf16_ok(q, k, v, o, a) ? 1 : 0;
+  return MX_OK;
 }
 
 int mx_attn_reference(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p, void* stream) {

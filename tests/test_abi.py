@@ -163,3 +163,16 @@ def test_workspace_layout_d64():
     per_wg = 4 * (8 * 4 * 64 * 4 + 8 * 64 * 2)
     assert L["cnt"] - L["split"] >= per_wg * L["split_units"] * L["split_parts"]
     assert L["cnt"] - L["split"] < per_wg * L["split_units"] * L["split_parts"] + 256
+
+
+def test_mfma_path_for_unaligned_strides():
+    """flash_attn runs the MFMA kernel for token strides that are not multiples of 8
+    elements (the reference's Aligned = false case) and for operands at 2-byte alignment;
+    an odd (not bf16-aligned) address takes the general kernel. Host-side query."""
+    from miroxen_amd.attention import flash_attn_uses_mfma
+    base = 1 << 20
+    for qs, ks in ((0, 0), (4 * 128 + 5, 2 * 128 + 7), (4 * 128 + 6, 2 * 128 + 8)):
+        p = AttnParams(Sq=100, Skv=300, Hq=4, Hkv=2, D=128, q_stride=qs, kv_stride=ks, o_stride=qs)
+        assert flash_attn_uses_mfma(base, base + 2, base + 6, base, p)
+    p = AttnParams(Sq=100, Skv=300, Hq=4, Hkv=2, D=128)
+    assert not flash_attn_uses_mfma(base + 1, base, base, base, p)

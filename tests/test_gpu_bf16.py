@@ -7,6 +7,7 @@ import torch
 
 import oracle
 from miroxen_amd import AttnParams, attn_reference, flash_attn
+from miroxen_amd.attention import flash_attn_uses_mfma
 from miroxen_amd.synth import CONFIGS, make_inputs
 from tests.helpers import cosine, max_abs, query_rows, reference_gate
 
@@ -76,6 +77,9 @@ def test_reference_suite(cuda, case):
     q, k, v, qs, ks, os_ = _make(Sq, Skv, Hq, Hkv, D, pad, mag, 1234 + Sq + Skv, cuda)
     p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=D, scale=scale, causal=causal, q_offset=off,
                    q_stride=qs if pad else 0, kv_stride=ks if pad else 0, o_stride=os_ if pad else 0)
+    # every case of the reference suite runs the MFMA kernel, the padded-stride (pad 5,
+    # 6: not multiples of 8 elements) cases included
+    assert flash_attn_uses_mfma(q, k, v, q, p)
     out, buf = _run(flash_attn, q, k, v, p, Sq, os_)
     rows = query_rows(Sq, Hq)
     got = _f32(out[rows, : Hq * D])

@@ -76,6 +76,7 @@ def test_supported(cuda):
     (130, 77, 2, 2, 128, 8, 2.0), (1088, 1088, 24, 24, 128, 0, 8.0),
     (1, 1, 1, 1, 64, 0, 0.0), (300, 300, 4, 4, 64, 0, 0.0), (257, 1000, 4, 2, 64, 0, 4.0),
     (130, 77, 2, 2, 64, 8, 2.0), (1088, 1088, 24, 24, 64, 0, 8.0),
+    (130, 77, 2, 2, 128, 5, 2.0), (257, 300, 4, 2, 64, 5, 4.0),  # strides not multiples of 8
 ])
 def test_prologue_bit_exact(cuda, Sq, Skv, Hq, Hkv, D, pad, kbias):
     print(f"prologue {Sq}x{Skv} H={Hq}/{Hkv} D={D} pad={pad}", flush=True)
@@ -195,8 +196,10 @@ def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
     rr_ref = rel_rms(ref_rule, exact)
     print(f"{seed_note} sage: cos(emu)={c_emu:.7f} maxabs(emu)={e_emu:.3g} cos(exact)={c_ex:.6f} relrms={rr:.4f} "
           f"relrms(reference rule)={rr_ref:.4f}", flush=True)
-    # emulator fed the same workspace: only accumulation order and the bf16 store differ
-    assert c_emu >= 0.99999 and e_emu <= 2e-2
+    # emulator fed the same workspace: accumulation order and the bf16 store differ, and
+    # the GPU's exp2 (v_exp_f32, within 1 ulp) against libm's can move a probability across
+    # an e4m3 rounding boundary, one e4m3 step (2^-4 relative) of that key's weight
+    assert c_emu >= 0.99999 and e_emu <= max(2e-2, 2.0 ** -4 * np.abs(emu).max())
     # Cosine >= 0.995 against exact attention, and the reference's 4 % rel-RMS gate
     # (tests/attention_fp8_test.cpp:65) unless the reference's own arithmetic (exact-max
     # emulator on the same quantized operands) already exceeds it on this input: then
@@ -310,7 +313,8 @@ def test_split_units_dead_parts_and_repeat(cuda):
 
 
 @pytest.mark.parametrize("Sq,Skv,Hq,Hkv,pad,kbias,masked", [
-    (130, 77, 2, 2, 8, 2.0, False), (300, 300, 4, 4, 0, 0.0, False), (257, 1000, 4, 2, 0, 4.0, True),
+    (130, 77, 2, 2, 8, 2.0, False), (130, 77, 2, 2, 5, 2.0, False), (300, 300, 4, 4, 0, 0.0, False),
+    (257, 1000, 4, 2, 0, 4.0, True),
     (4352, 4352, 24, 24, 0, 8.0, True),
 ])
 def test_sage_d64(cuda, Sq, Skv, Hq, Hkv, pad, kbias, masked):
@@ -350,5 +354,5 @@ def test_sage_d64(cuda, Sq, Skv, Hq, Hkv, pad, kbias, masked):
     c_ex, rr, rr_ref = cosine(got, exact), rel_rms(got, exact), rel_rms(ref_rule, exact)
     print(f"  cos(emu)={c_emu:.7f} maxabs(emu)={e_emu:.3g} cos(exact)={c_ex:.6f} relrms={rr:.4f} "
           f"relrms(reference rule)={rr_ref:.4f}", flush=True)
-    assert c_emu >= 0.99999 and e_emu <= 2e-2
+    assert c_emu >= 0.99999 and e_emu <= max(2e-2, 2.0 ** -4 * np.abs(emu).max())  # as _sage_vs_oracle
     assert c_ex >= 0.995 and rr < max(0.04, rr_ref + 0.0025)
