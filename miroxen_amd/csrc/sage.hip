@@ -48,7 +48,7 @@ __device__ __forceinline__ u32x2 quant8(const float (&x)[8], float inv) {
 }
 
 constexpr int kStatChunk = 128;  // tokens staged in LDS per step of a stats block
-constexpr int kFoldNb = 32;      // statistics partials per head up to which prep_kv_quant finalizes them
+constexpr int kFoldNb = 32;       // statistics partials per head up to which prep_kv_quant finalizes them
 
 // NRM >= 0: q and k are the raw projections; every row gets the per-head RMS-norm
 // + RoPE of head_norm_rope (nq / nk, nr128_row with rope mode NRM) and its bf16
@@ -103,11 +103,25 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
               *reinterpret_cast<const u32x4*>(v + (c0 + r) * p.kv_stride + int64_t(h) * D + cc);
         }
       } else {
-        for (int i = tid; i < rows * (D / 8); i += 256) {
-          const int r = i / (D / 8), c = (i % (D / 8)) * 8;
+        // every load of the chunk in flight before the first LDS store (rows past the
+        // chunk's end are not loaded; their LDS rows are never summed)
+        constexpr int NL = kStatChunk * (D / 8) / 256;
+        u32x4 kr[NL], vr[NL];
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+          const int i = tid + 256 * u, r = i / (D / 8), c = (i % (D / 8)) * 8;
           const int64_t g = (c0 + r) * p.kv_stride + int64_t(h) * D + c;
-          *reinterpret_cast<u32x4*>(&kt[r * D + c]) = *reinterpret_cast<const u32x4*>(k + g);
-          *reinterpret_cast<u32x4*>(&vt_[r * D + c]) = *reinterpret_cast<const u32x4*>(v + g);
+          kr[u] = vr[u] = u32x4{0, 0, 0, 0};
+          if (r < rows) {
+            kr[u] = *reinterpret_cast<const u32x4*>(k + g);
+            vr[u] = *reinterpret_cast<const u32x4*>(v + g);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+          const int i = tid + 256 * u, r = i / (D / 8), c = (i % (D / 8)) * 8;
+          *reinterpret_cast<u32x4*>(&kt[r * D + c]) = kr[u];
+          *reinterpret_cast<u32x4*>(&vt_[r * D + c]) = vr[u];
         }
       }
       __syncthreads();
