@@ -231,7 +231,7 @@ __device__ __forceinline__ uint32_t e4m3x2_sat(float a, float b) {
 
 // Per (64-key tile, head): K - mean -> INT8 (one scale per tile) and V -> e4m3
 // transposed to [H][D][skv_pad] in natural key order. Thread tid owns channel
-// chunk tid % (D/8) (8 channels) of rows tid / (D/8) + (2048/D) i, i < D/32.
+// chunk tid % (D/8) (8 channels) of the D/32 consecutive keys from (tid / (D/8)) D/32.
 // fold_nb > 0: prep_finalize is folded in (short sequences, few partials): every
 // work-group sums its head's fold_nb partials itself, work-groups of tile 0 store
 // the head's km / va, and work-group (0, 0) zeroes the attention kernel's split
@@ -250,7 +250,7 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
   static_assert(NRM < 0 || D == 128, "the fused norm/rope prologue is built for D = 128");
   constexpr int CPR = D / 8, RPP = 256 / CPR, NI = kKvPad / RPP;  // chunks per row, rows per pass, passes
   const int h = blockIdx.y, k0 = blockIdx.x * kKvPad, tid = threadIdx.x;
-  const int c = (tid % CPR) * 8, r0 = tid / CPR;
+  const int c = (tid % CPR) * 8, kr0 = (tid / CPR) * NI;  // channels c..c+7 of keys kr0..kr0+NI-1
   const float* kmh = km + h * D;
   const float* vah = va + h * D;
   if (fold_nb > 0) {
@@ -281,7 +281,7 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
   u32x4 kraw[NI], vraw[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    const int64_t row = k0 + r0 + RPP * i;
+    const int64_t row = k0 + kr0 + i;
     kraw[i] = vraw[i] = u32x4{0, 0, 0, 0};
     if (row < p.Skv) {
       const int64_t g = row * p.kv_stride + int64_t(h) * D + c;
@@ -293,7 +293,7 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
   float x[NI][8], am = 0.f;
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    const int64_t row = k0 + r0 + RPP * i;
+    const int64_t row = k0 + kr0 + i;
     const bool ok = row < p.Skv;
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[i][j] = bf2f(uint16_t(kraw[i][j >> 1] >> ((j & 1) * 16)));
@@ -304,19 +304,25 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
       am = fmaxf(am, fabsf(x[i][j]));
     }
   }
-  // V -> e4m3 into the transposed LDS tile while the K amax reduces
+  // V -> e4m3 into the transposed LDS tile while the K amax reduces: the thread's NI
+  // consecutive keys of each of its 8 channels go out as one NI-byte LDS write; the
+  // 16-byte key chunk q of channel row d sits at chunk q ^ ((d >> 4) & 3), which with
+  // the 80-byte row pitch spreads a wave's writes over 32 banks
+  static_assert(NI == 4 || NI == 2, "keys per thread");
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int key = r0 + RPP * i;
-    const bool ok = k0 + key < p.Skv;
+  for (int j = 0; j < 8; ++j) {
+    float f[NI];
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-      const float f0 = ok && vsc[j] > 0.f ? bf2f(uint16_t(vraw[i][j >> 1])) * vsc[j] : 0.f;
-      const float f1 = ok && vsc[j + 1] > 0.f ? bf2f(uint16_t(vraw[i][j >> 1] >> 16)) * vsc[j + 1] : 0.f;
-      const uint32_t pk = e4m3x2_sat(f0, f1);
-      tile[c + j][key] = uint8_t(pk);
-      tile[c + j + 1][key] = uint8_t(pk >> 8);
+    for (int i = 0; i < NI; ++i) {
+      const bool ok = k0 + kr0 + i < p.Skv && vsc[j] > 0.f;
+      f[i] = ok ? bf2f(uint16_t(vraw[i][j >> 1] >> ((j & 1) * 16))) * vsc[j] : 0.f;
     }
+    const int d = c + j;
+    uint8_t* dst = &tile[d][16 * ((kr0 >> 4) ^ ((d >> 4) & 3)) + (kr0 & 15)];
+    if constexpr (NI == 4)
+      *reinterpret_cast<uint32_t*>(dst) = e4m3x2_sat(f[0], f[1]) | (e4m3x2_sat(f[2], f[3]) << 16);
+    else
+      *reinterpret_cast<uint16_t*>(dst) = uint16_t(e4m3x2_sat(f[0], f[1]));
   }
   am = wave_max(am);
   if ((tid & 63) == 0) red[tid >> 6] = am;
@@ -325,7 +331,7 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
   const float inv = am > 0.f ? 127.f / am : 0.f;
 #pragma unroll
   for (int i = 0; i < NI; ++i)
-    *reinterpret_cast<u32x2*>(ki + (int64_t(h) * skv_pad + k0 + r0 + RPP * i) * D + c) = quant8(x[i], inv);
+    *reinterpret_cast<u32x2*>(ki + (int64_t(h) * skv_pad + k0 + kr0 + i) * D + c) = quant8(x[i], inv);
   if (tid == 0) ks[int64_t(h) * (skv_pad / kKvPad) + blockIdx.x] = am / 127.f * 1.f;
   // tile table of the attention kernel: liveness bits of the tile's 64 keys (mask and
   // tail) and its K scale, negated when some key is dead (the kernel's loop branches on
@@ -343,7 +349,7 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
   for (int i = tid; i < D * (kKvPad / 16); i += 256) {
     const int d = i / (kKvPad / 16), u = i % (kKvPad / 16);
     *reinterpret_cast<u32x4*>(vt + (int64_t(h) * D + d) * skv_pad + k0 + u * 16) =
-        *reinterpret_cast<const u32x4*>(&tile[d][u * 16]);
+        *reinterpret_cast<const u32x4*>(&tile[d][16 * (u ^ ((d >> 4) & 3))]);
   }
 }
 
