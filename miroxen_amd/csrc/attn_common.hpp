@@ -82,6 +82,17 @@ __device__ __forceinline__ void buf2lds16(__amdgpu_buffer_rsrc_t r, uint32_t vof
 
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// 16-byte device-scope (sc1) buffer store, then two wait states. A VALU write to the
+// data registers of a store of more than 8 bytes must not follow it directly (the
+// store may read its data after that write); the compiler for gfx950 schedules such
+// writes right after the store (seen: the next 16-byte group converted into the same
+// registers, with values of that group stored in some lanes), so this store carries
+// its own wait states.
+__device__ __forceinline__ void store_b128_sc1(u32x4 d, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  asm volatile("buffer_store_dwordx4 %0, %1, %2, %3 offen sc1\n\ts_nop 1" ::"v"(d), "v"(voff), "s"(r), "s"(soff)
+               : "memory");
+}
+
 // Work-group barrier without __syncthreads()'s memory fence: the fence drains
 // every outstanding global load (vmcnt(0)), which would serialize a multi-stage
 // prefetch. Callers order LDS-DMA completion themselves with counted vmcnt waits;

@@ -542,10 +542,9 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[D / 32], float m, floa
     for (int j = 0; j < D / 16; ++j) {  // group j: acc[j / 2][(j & 1) * 8 .. + 7]
       const f32x16& a = acc[j >> 1];
       const int b = (j & 1) * 8;
-      __builtin_amdgcn_raw_buffer_store_b128(
-          u32x4{h2(a[b] * inv, a[b + 1] * inv), h2(a[b + 2] * inv, a[b + 3] * inv), h2(a[b + 4] * inv, a[b + 5] * inv),
-                h2(a[b + 6] * inv, a[b + 7] * inv)},
-          rp, lacc + uint32_t(j) * 1024u, mine, kSc1);
+      store_b128_sc1(u32x4{h2(a[b] * inv, a[b + 1] * inv), h2(a[b + 2] * inv, a[b + 3] * inv),
+                           h2(a[b + 4] * inv, a[b + 5] * inv), h2(a[b + 6] * inv, a[b + 7] * inv)},
+                     rp, lacc + uint32_t(j) * 1024u, mine);
     }
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m, l}), rp, lml, mine, kSc1);
     // Publication order without a release fence: every lane waits until its sc1
