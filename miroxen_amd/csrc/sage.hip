@@ -648,10 +648,13 @@ sage_attn_gen(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, cons
   if (int(blockIdx.x) < sp.full) {
     L = xcd_remap(blockIdx.x, sp.full);
   } else {
-    // part-major order (part 0 of every split unit, then part 1, ...): the last
-    // arrivals, which also merge, fall in the grid's last batch instead of delaying
-    // the dispatch of the batches before it
-    const int j = int(blockIdx.x) - sp.full, nsu = (int(gridDim.x) - sp.full) / sp.parts;
+    // part-major order (part 0 of every split unit, then part 1, ...), XCD-grouped:
+    // each XCD runs a contiguous run of that order, i.e. one key range of consecutive
+    // units (mostly one or two heads), so its L2 holds the K/V^T tiles they share
+    // (unit su on XCD su % 8 spread every head over all eight L2s: 3.3x the
+    // algorithmic HBM bytes)
+    const int nsu = (int(gridDim.x) - sp.full) / sp.parts;
+    const int j = xcd_remap(int(blockIdx.x) - sp.full, int(gridDim.x) - sp.full);
     part = j / nsu;
     su = j - part * nsu;
     L = sp.full + su;
@@ -802,8 +805,9 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   int L, tb = 0, nt = nkt, su = 0, part = -1;
   if (int(blockIdx.x) < sp.full) {
     L = xcd_remap(blockIdx.x, sp.full);
-  } else {  // split units, part-major (see sage_attn_gen)
-    const int j = int(blockIdx.x) - sp.full, nsu = (int(gridDim.x) - sp.full) / sp.parts;
+  } else {  // split units, part-major, XCD-grouped (see sage_attn_gen)
+    const int nsu = (int(gridDim.x) - sp.full) / sp.parts;
+    const int j = xcd_remap(int(blockIdx.x) - sp.full, int(gridDim.x) - sp.full);
     part = j / nsu;
     su = j - part * nsu;
     L = sp.full + su;
