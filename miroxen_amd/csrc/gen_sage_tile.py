@@ -84,7 +84,7 @@ V_LV2 = 235            # per-lane offset of the second V^T op (16 channel rows f
 ALPHA = (239, 225)     # rescale factor of the tiles of parity 0 / 1
 
 KTILE = 8192          # bytes per K or V^T tile slot
-HEADROOM = 2.0        # lazy-max headroom H (log2 units)
+HEADROOM = 3.0        # lazy-max headroom H (log2 units)
 LOG2_448 = 8.807354922057604
 
 

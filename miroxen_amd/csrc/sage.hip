@@ -398,7 +398,7 @@ struct SageSplit {
   float* part;      // partials, split_floats(NW, D) per split work-group
   int* cnt;         // arrival counter per split unit
 };
-constexpr float kSageHeadroom = 2.f;
+constexpr float kSageHeadroom = 3.f;
 constexpr int kScoreBias = 0x4B400000;  // bits of 12582912.0f = 1.5 * 2^23
 constexpr i32x16 kScoreBias16 = {kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
                                  kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,

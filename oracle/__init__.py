@@ -150,7 +150,7 @@ def v_quant(v, Skv, Hkv, D, kv_stride, skv_pad, vamax):
 
 
 # Lazy-max headroom of the GPU Sage kernel (log2 units); 0 = reference exact-max rule.
-KERNEL_HEADROOM = 2.0
+KERNEL_HEADROOM = 3.0
 
 
 def sage_emulate(qi, ki, vt, qs, ks, vamax, Sq, Skv, Hq, Hkv, D, kv_valid=None, rows=None, threads=0,

@@ -328,7 +328,7 @@ static void or_sage_range(const int8_t* qr, float qscale, const int8_t* ki, cons
     const float tmax = (float)im * sc;
     /* headroom 0: next = max(m, tmax), the reference rule (:327). headroom H > 0:
      * lazy max, m moves only when the tile max exceeds it by more than H, and P
-     * carries 2^-H so it stays <= 448 (this build's kernel uses H = 2). */
+     * carries 2^-H so it stays <= 448 (this build's kernel uses H = 3). */
     float next = tmax > m + headroom ? tmax : m;
     float alpha = m == -INFINITY ? 0.f : (float)exp2((double)(m - next));
     m = next;
