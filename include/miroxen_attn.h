@@ -78,6 +78,16 @@ int mx_flash_attn_fp8(const void* q, const void* k, const void* v, void* o, cons
 int mx_flash_attn_uses_mfma(const void* q, const void* k, const void* v, const void* o, const mx_attn_params* p,
                             int* mfma);
 
+/* No counterpart in the reference (a diagnostic query): how mx_flash_attn splits the
+ * work of these parameters on a device with `cus` compute units (cus <= 0: the current
+ * device). The first *full units (head, 256-query tile) run whole; each of the last
+ * *units units runs as *parts key ranges whose partial outputs a merge kernel combines
+ * (parts == 1: no split). A split call keeps its partials in a library-held device
+ * region (allocated on first use, grown on demand, one per device, calls ordered by an
+ * event); under stream capture, for causal calls and when that region cannot be
+ * allocated the call runs unsplit. Launches nothing. */
+int mx_flash_attn_split_plan(const mx_attn_params* p, int cus, int* full, int* units, int* parts);
+
 /* No counterpart in the reference. For callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc):
  * mx_flash_attn_fp8 with the workspace taken from a fixed library-owned device scratch

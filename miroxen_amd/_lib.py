@@ -18,7 +18,8 @@ MX_OK, MX_E_INVALID, MX_E_HIP, MX_E_UNSUPPORTED = 0, -1, -2, -3
 # Exported symbols, in header order (tests check every one is exported).
 SYMBOLS = (
     "mx_flash_attn", "mx_flash_attn_fp8_workspace", "mx_flash_attn_fp8_supported",
-    "mx_flash_attn_fp8_ok", "mx_flash_attn_fp8", "mx_flash_attn_uses_mfma", "mx_flash_attn_fp8_noalloc",
+    "mx_flash_attn_fp8_ok", "mx_flash_attn_fp8", "mx_flash_attn_uses_mfma", "mx_flash_attn_split_plan",
+    "mx_flash_attn_fp8_noalloc",
     "mx_attn_reference", "mx_sage_layout_of",
     "mx_sage_quantize", "mx_sage_attend", "mx_last_error", "mx_version", "mx_head_norm_rope",
     "mx_sage_quantize_norm_rope", "mx_flash_attn_fp8_norm_rope", "mx_sage_quantize_qgroup",
@@ -69,6 +70,7 @@ def load():
         "mx_flash_attn_fp8": ([vp, vp, vp, vp, P, vp, vp], ctypes.c_int),
         "mx_flash_attn_fp8_noalloc": ([vp, vp, vp, vp, P, vp], ctypes.c_int),
         "mx_flash_attn_uses_mfma": ([vp, vp, vp, vp, P, ip], ctypes.c_int),
+        "mx_flash_attn_split_plan": ([P, ctypes.c_int, ip, ip, ip], ctypes.c_int),
         "mx_attn_reference": ([vp, vp, vp, vp, P, vp], ctypes.c_int),
         "mx_sage_layout_of": ([P, ctypes.POINTER(CLayout)], ctypes.c_int),
         "mx_sage_quantize": ([vp, vp, vp, P, vp, vp], ctypes.c_int),

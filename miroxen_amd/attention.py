@@ -93,6 +93,17 @@ def flash_attn_uses_mfma(q, k, v, o, p: AttnParams) -> bool:
     return bool(res.value)
 
 
+def flash_attn_split_plan(p: AttnParams, cus: int = 0) -> tuple:
+    """(full, units, parts): how flash_attn splits this shape's grid on a device with
+    `cus` compute units (0: the current device); a diagnostic query with no counterpart
+    in the reference."""
+    c = p.c()
+    f, u, s = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+    _lib.check(_lib.load().mx_flash_attn_split_plan(ctypes.byref(c), int(cus), ctypes.byref(f), ctypes.byref(u),
+                                                    ctypes.byref(s)))
+    return f.value, u.value, s.value
+
+
 def flash_attn_fp8_ok(q, k, v, o, p: AttnParams) -> bool:
     """Reference mx::flash_attn_fp8_ok (src/kernels/attention_fp8.cu:484-486)."""
     c = p.c()

@@ -19,6 +19,7 @@ hipError_t launch_head_norm_rope(const uint16_t*, int64_t, int64_t, int64_t, int
                                  hipStream_t);
 hipError_t launch_flash_bf16(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*,
                                   const mx_attn_params&, hipStream_t);
+int flash_bf16_split_plan(const mx_attn_params&, int cus, int* full, int* units, int* parts);
 hipError_t launch_naive_attn(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, const mx_attn_params&,
                              hipStream_t);
 mx_sage_layout sage_layout(const mx_attn_params&);
@@ -183,6 +184,19 @@ int mx_flash_attn_uses_mfma(const void* q, const void* k, const void* v, const v
   int rc = validate(q, k, v, o, p, &a);
   if (rc) return rc;
   *mfma = fast_bf16_ok(q, k, v, o, a) ? 1 : 0;
+  return MX_OK;
+}
+
+int mx_flash_attn_split_plan(const mx_attn_params* p, int cus, int* full, int* units, int* parts) {
+  if (!p || !full || !units || !parts) return fail(MX_E_INVALID, "flash_attn_split_plan: null argument");
+  if (p->Sq <= 0 || p->Skv <= 0 || p->Hq <= 0) return fail(MX_E_INVALID, "flash_attn_split_plan: empty shape");
+  if (cus <= 0) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_status(e, "flash_attn_split_plan");
+  }
+  mxa::flash_bf16_split_plan(*p, cus, full, units, parts);
   return MX_OK;
 }
 

@@ -27,6 +27,7 @@
 //    than all waves in lockstep. Within an MFMA phase, sched_group_barrier keeps
 //    LDS operand reads a few MFMAs ahead of use (kKPrefetch / kVPrefetch).
 //  * Work-groups are remapped so one head's query tiles share an XCD (and its L2).
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -340,10 +341,59 @@ __device__ __forceinline__ void store_block(const QBlock<DH>& X, uint16_t* o, co
 // K(t+2) and V(t+1) go into the buffers of K(t) and V(t-1), both last read in
 // period 2t; group A issues all of their DMA ops during its MFMA period 2t+1
 // (8 per wave, one per four MFMAs), and waits for them at the top of tile t+1.
-template <int DH, bool CAUSAL>
+// Key-range split of the grid's last round (non-causal). The main launch runs the
+// first `full` units (head, 256-query tile) whole; a second launch of the same kernel
+// (SPLIT) runs each of the last `units` units as `parts` work-groups over consecutive
+// key-tile ranges, and each writes its normalised partial output, scaled into fp16's
+// range per query, with (m, l, scale) to a device region; bf16_split_merge combines
+// the parts. Part-major work-group order: the work-groups of one XCD run one key range
+// of consecutive units (mostly one head), so its L2 serves the K/V tiles they share.
+struct BfSplit {
+  uint16_t* po;  // [units][parts][256 queries][DH] fp16 partial outputs (o / scale)
+  f32x4* ml;     // [units][parts][256 queries] {m (log2 units), l, scale, 0}
+  int full, units, parts;
+};
+
+// Normalised partial of one 32-query block: o = acc / l, stored as fp16(o * 2^(15-e))
+// with 2^(e-15) beside it, where e is the exponent of the query's largest |o| (so
+// every stored value lies below 2^15 and keeps fp16's 11 significant bits relative
+// to the row's largest). A query with no live key in the range stores l = 0.
+template <int DH>
+__device__ __forceinline__ void store_partial(const QBlock<DH>& X, const BfSplit& sp, int su, int part, int lrow,
+                                              const Lane& ln) {
+  float amax = 0.f;  // over the stored channels (D = 72: 72..95 hold padding products)
+#pragma unroll
+  for (int db = 0; db < X.NB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (DH % 32 == 0 || db * 32 + (i >> 2) * 8 < DH) amax = fmaxf(amax, __builtin_fabsf(X.acc[db][i]));
+  amax = fmaxf(amax, other_half(amax));
+  const float inv = X.l > 0.f ? 1.f / X.l : 0.f;
+  int e = __builtin_amdgcn_frexp_expf(amax * inv);
+  e = e < -100 ? -100 : (e > 140 ? 140 : e);
+  const float sc = __builtin_ldexpf(inv, 15 - e);
+  const size_t blk = size_t(su) * sp.parts + part;
+  uint16_t* dst = sp.po + (blk * 256 + lrow) * DH + ln.h * 4;
+#pragma unroll
+  for (int db = 0; db < X.NB; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (DH % 32 != 0 && db * 32 + g * 8 >= DH) continue;
+      using h2 = __attribute__((ext_vector_type(2))) _Float16;
+      const h2 a = __builtin_convertvector((f32x2){X.acc[db][g * 4] * sc, X.acc[db][g * 4 + 1] * sc}, h2);
+      const h2 b = __builtin_convertvector((f32x2){X.acc[db][g * 4 + 2] * sc, X.acc[db][g * 4 + 3] * sc}, h2);
+      u32x2 w = {__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+      *reinterpret_cast<u32x2*>(dst + db * 32 + g * 8) = w;
+    }
+  // both wave halves store the query's (identical) record: a branch on the half here
+  // changes the compiler's schedule of the whole tile loop for the worse
+  sp.ml[blk * 256 + lrow] = f32x4{X.m, X.l, __builtin_ldexpf(1.f, e - 15), 0.f};
+}
+
+template <int DH, bool CAUSAL, bool SPLIT>
 __global__ void __launch_bounds__(512, 1)
 flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-              uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign) {
+              uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign, BfSplit sp) {
   using Dm = Dims<DH>;
   constexpr int NW = 8, QT = NW * 32;
   constexpr int LDK = (Dm::KOPS + 3) / 4, LDV = (Dm::VOPS + 3) / 4;  // loop DMA ops per group-A wave
@@ -357,12 +407,21 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const bool group_a = wave < 4;
   const int ntq = (p.Sq + QT - 1) / QT;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int Lx = xcd_remap(blockIdx.x, gridDim.x);
+  int L = Lx, su = 0, part = 0;
+  if constexpr (SPLIT) {  // part-major: su = split unit, part = key range
+    part = Lx / sp.units;
+    su = Lx - part * sp.units;
+    L = sp.full + su;
+  }
   // causal: query tiles with the most key tiles first
   const int head = L / ntq, qtile = CAUSAL ? ntq - 1 - L % ntq : L % ntq;
   const int kvh = head / (p.Hq / p.Hkv);
   const int q0 = qtile * QT + wave * 32;
-  const int nt = tiles_needed<CAUSAL>(p, qtile * QT, QT);
+  const int ntk = tiles_needed<CAUSAL>(p, qtile * QT, QT);
+  // key tiles [tb, nt) of this work-group
+  const int tb = SPLIT ? int(int64_t(part) * ntk / sp.parts) : 0;
+  const int nt = SPLIT ? int(int64_t(part + 1) * ntk / sp.parts) : ntk;
   const int64_t kvbase = int64_t(kvh) * DH;
   const TileAddr ta8 = tile_addr<8>(p, wave_u, ln.lane);      // prologue: all 8 waves load
   const TileAddr ta4 = tile_addr<4>(p, wave_u & 3, ln.lane);  // loop: group A loads
@@ -373,9 +432,9 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
     store_block(A, o, p, q0, head, ln);
     return;
   }
-  load_tile<NW, false, DH>(k, 0, kb0, p, kvbase, wave_u, ta8);
-  load_tile<NW, true, DH>(v, 0, vb0, p, kvbase, wave_u, ta8);
-  if (nt > 1) load_tile<NW, false, DH>(k, 1, kb1, p, kvbase, wave_u, ta8);
+  load_tile<NW, false, DH>(k, tb, kb0, p, kvbase, wave_u, ta8);
+  load_tile<NW, true, DH>(v, tb, vb0, p, kvbase, wave_u, ta8);
+  if (nt > tb + 1) load_tile<NW, false, DH>(k, tb + 1, kb1, p, kvbase, wave_u, ta8);
   qblock_init(A, q, p, q0, head, ln, qsign);
   build_live<NW, KT>(live_tiles, p, nt, wave, ln.lane);
 
@@ -415,8 +474,8 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
     sched_k<2 * Dm::NC, 0>();
   }
   block_sync();
-  if (group_a) {    // period 0: A softmax(0), B S_B(0)
-    valu_part(0);
+  if (group_a) {    // period 0: A softmax(tb), B S_B(tb)
+    valu_part(tb);
   } else {
     scores(kb0, A, ln);
     sched_k<2 * Dm::NC, 0>();
@@ -436,19 +495,130 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
       mfma_part(t, kc1, vcur, kfree, vfree, std::false_type{});
     }
   };
-  for (int t = 0; t < nt; t += 2) {
+  for (int t = tb; t < nt; t += 2) {
     tile(t, kb1, vb0, kb0, vb1);
     if (t + 1 < nt) tile(t + 1, kb0, vb1, kb1, vb0);
   }
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
-  store_block(A, o, p, q0, head, ln);
+  if constexpr (SPLIT) store_partial(A, sp, su, part, wave * 32 + ln.n, ln);
+  else store_block(A, o, p, q0, head, ln);
+}
+
+// Merge of the split units' parts: one thread per (query, 8 channels). With
+// M = max m_i and c_i = l_i 2^(m_i - M), o = sum c_i scale_i o_i / sum c_i (parts
+// whose keys were all dead have l_i = 0 and drop out; no live key at all gives 0).
+template <int DH>
+__global__ void __launch_bounds__(256)
+bf16_split_merge(uint16_t* __restrict__ o, mx_attn_params p, BfSplit sp) {
+  constexpr int G = DH / 8, QT = 256;
+  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t rowg = idx / G;
+  const int g = int(idx - rowg * G);
+  if (rowg >= int64_t(sp.units) * QT) return;
+  const int su = int(rowg / QT), lrow = int(rowg % QT);
+  const int ntq = (p.Sq + QT - 1) / QT;
+  const int L = sp.full + su, head = L / ntq, row = (L % ntq) * QT + lrow;
+  if (row >= p.Sq) return;
+  float M = -__builtin_inff();
+  for (int i = 0; i < sp.parts; ++i) {
+    const f32x4 t = sp.ml[(size_t(su) * sp.parts + i) * QT + lrow];
+    if (t[1] > 0.f) M = fmaxf(M, t[0]);
+  }
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, den = 0.f;
+  for (int i = 0; i < sp.parts; ++i) {
+    const size_t blk = (size_t(su) * sp.parts + i) * QT + lrow;
+    const f32x4 t = sp.ml[blk];
+    if (!(t[1] > 0.f)) continue;
+    const float cw = t[1] * __builtin_amdgcn_exp2f(t[0] - M);
+    den += cw;
+    const float f = cw * t[2];
+    using h8 = __attribute__((ext_vector_type(8))) _Float16;
+    const h8 x = *reinterpret_cast<const h8*>(sp.po + blk * DH + g * 8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] += f * float(x[j]);
+  }
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  u32x4 w;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(acc[2 * j] * inv, acc[2 * j + 1] * inv);
+  uint32_t* d = reinterpret_cast<uint32_t*>(o + int64_t(row) * p.o_stride + int64_t(head) * DH + g * 8);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) d[j] = w[j];
 }
 
 }  // namespace
 
+namespace {
+
+// Split plan for a non-causal grid of U units on C CUs (one work-group per CU). The
+// chip is power-limited: a CU runs a 64-key tile in ~1.29 us (D = 128) while at most
+// ~165 CUs are busy, and the clock drops as more are (~2.0 us per tile with all 256
+// busy; measured on MI355X). So the grid's last, partly filled round of r = U mod C
+// units costs nearly as much as a full one only when r is small; for r near C its CUs
+// run faster and splitting buys little. The estimate below compares that round with
+// splitting its units into S key ranges: rounds of min(C, remaining parts) busy CUs,
+// each part nt/S tiles plus ~2 tiles of fixed work (Q load, first tiles, partial
+// store), then the merge (partial bytes at ~3 TB/s plus ~4 us) and ~3 us for the
+// second launch when whole rounds precede it. S minimises the estimate; no split
+// unless it wins by 5 %. Measured: U = 2..32 units 1.9-3.2x faster, config-2 shape
+// (408 units, r = 152) and 120 units of 17 tiles unsplit.
+struct Bf16Plan {
+  int full, units, parts;
+};
+constexpr int kBfMaxParts = 8;
+Bf16Plan bf16_plan(const mx_attn_params& p, int C) {
+  constexpr int QT = 256;
+  const int64_t U64 = int64_t((p.Sq + QT - 1) / QT) * p.Hq;
+  const int nt = (p.Skv + KT - 1) / KT;
+  Bf16Plan pl{int(U64), 0, 1};
+  if (p.causal || C <= 0 || U64 >= 0x7fffffff) return pl;
+  const int U = int(U64), r = U % C;
+  if (r == 0) return pl;
+  const double t0 = 1.29e-6 * (0.4 + 0.6 * p.D / 128.0);  // s per tile per CU, <= kBusyFast busy CUs
+  constexpr double kBusyFast = 165.0;
+  auto tile_s = [&](int busy) { return t0 * (busy > kBusyFast ? busy / kBusyFast : 1.0); };
+  const double whole = nt * tile_s(r);
+  double best = 0.95 * whole;
+  for (int S = 2; S <= kBfMaxParts && S * 4 <= nt; ++S) {
+    double cost = U > r ? 3e-6 : 0.0;
+    for (int64_t left = int64_t(r) * S; left > 0; left -= C)
+      cost += (double(nt) / S + 2.0) * tile_s(int(left < C ? left : C));
+    cost += double(r) * S * QT * (2 * p.D + 16) / 3e12 + 4e-6;
+    if (cost < best) best = cost, pl.parts = S;
+  }
+  if (pl.parts > 1) pl.full = U - r, pl.units = r;
+  return pl;
+}
+size_t bf16_split_bytes(const Bf16Plan& pl, int D) {
+  const size_t blocks = size_t(pl.units) * pl.parts * 256;
+  return blocks * sizeof(f32x4) + (blocks * D * 2 + 255) / 256 * 256;
+}
+
+// Library-held region for the split partials, one per device, grown on demand. Calls
+// that use it are ordered by a per-device event (a call on another stream waits for
+// the previous split's merge), so concurrent calls never share it. The split is not
+// used under stream capture or when the region cannot be allocated: the call then runs
+// as one launch.
+constexpr int kMaxDev = 64;
+struct SplitRegion {
+  std::mutex mu;
+  void* buf = nullptr;
+  size_t bytes = 0;
+  hipEvent_t done = nullptr;
+  int cus = 0;
+};
+SplitRegion g_split[kMaxDev];
+
+}  // namespace
+
+int flash_bf16_split_plan(const mx_attn_params& p, int cus, int* full, int* units, int* parts) {
+  const Bf16Plan pl = bf16_plan(p, cus);
+  *full = pl.full, *units = pl.units, *parts = pl.parts;
+  return 0;
+}
+
 // Launch the fast path. Preconditions (checked by the caller): D in {64, 72, 128},
-// q/k/v 16-byte aligned with token strides % 8 == 0, o 4-byte aligned with
-// o_stride % 2 == 0, Skv * kv_stride * 2 < 2^32.
+// q/k/v/o 2-byte aligned, Skv * kv_stride * 2 < 2^32.
 hipError_t launch_flash_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                              const mx_attn_params& p, hipStream_t s) {
   const float c = __builtin_fabsf(p.scale) * kLog2e;
@@ -457,18 +627,74 @@ hipError_t launch_flash_bf16(const uint16_t* q, const uint16_t* k, const uint16_
   const int ntq = (p.Sq + QT - 1) / QT;
   const int64_t blocks = int64_t(ntq) * p.Hq;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  const dim3 grid{unsigned(blocks)}, block{512};
-  auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, 0, s, q, k, v, o, p, c, qsign); };
+  if (p.D != 128 && p.D != 64 && p.D != 72) return hipErrorInvalidValue;
   const bool cz = p.causal != 0;
-  switch (p.D) {
-    case 128:
-      cz ? go(flash_bf16_pp<128, true>) : go(flash_bf16_pp<128, false>);
-      break;
-    case 64: cz ? go(flash_bf16_pp<64, true>) : go(flash_bf16_pp<64, false>); break;
-    case 72: cz ? go(flash_bf16_pp<72, true>) : go(flash_bf16_pp<72, false>); break;
-    default: return hipErrorInvalidValue;
+
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  SplitRegion* R = dev >= 0 && dev < kMaxDev ? &g_split[dev] : nullptr;
+  std::unique_lock<std::mutex> lock;
+  Bf16Plan pl{int(blocks), 0, 1};
+  if (R && !cz) {
+    lock = std::unique_lock<std::mutex>(R->mu);
+    if (!R->cus) {
+      int n = 0;
+      if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) R->cus = n;
+    }
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
+    if (cap == hipStreamCaptureStatusNone) pl = bf16_plan(p, R->cus);
+    if (pl.parts > 1) {
+      const size_t need = bf16_split_bytes(pl, p.D);
+      if (R->bytes < need) {
+        if (R->buf) {  // the previous region may still be read by an earlier merge
+          if (R->done && hipEventSynchronize(R->done) != hipSuccess) pl = Bf16Plan{int(blocks), 0, 1};
+          else if (hipFree(R->buf) == hipSuccess) R->buf = nullptr, R->bytes = 0;
+        }
+        if (pl.parts > 1 && !R->buf) {
+          void* b = nullptr;
+          if (hipMalloc(&b, need) == hipSuccess) R->buf = b, R->bytes = need;
+          else (void)hipGetLastError();
+        }
+        if (R->bytes < need) pl = Bf16Plan{int(blocks), 0, 1};
+      }
+      if (pl.parts > 1 && !R->done && hipEventCreateWithFlags(&R->done, hipEventDisableTiming) != hipSuccess)
+        pl = Bf16Plan{int(blocks), 0, 1};
+    }
   }
-  return hipGetLastError();
+
+  BfSplit sp{nullptr, nullptr, pl.full, pl.units, pl.parts};
+  auto run = [&](auto kern, int64_t n) {
+    if (n > 0) hipLaunchKernelGGL(kern, dim3(unsigned(n)), dim3(512), 0, s, q, k, v, o, p, c, qsign, sp);
+  };
+  auto go = [&](auto DHc) -> hipError_t {
+    constexpr int DH = decltype(DHc)::value;
+    if (cz) {
+      run(flash_bf16_pp<DH, true, false>, blocks);
+      return hipGetLastError();
+    }
+    run(flash_bf16_pp<DH, false, false>, pl.full);
+    if (pl.parts > 1) {
+      hipError_t e2 = hipStreamWaitEvent(s, R->done, 0);
+      if (e2 != hipSuccess) return e2;
+      const size_t blocks_ml = size_t(pl.units) * pl.parts * 256;
+      sp.ml = static_cast<f32x4*>(R->buf);
+      sp.po = reinterpret_cast<uint16_t*>(static_cast<char*>(R->buf) + blocks_ml * sizeof(f32x4));
+      run(flash_bf16_pp<DH, false, true>, int64_t(pl.units) * pl.parts);
+      const int64_t threads = int64_t(pl.units) * QT * (DH / 8);
+      hipLaunchKernelGGL(bf16_split_merge<DH>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, o, p, sp);
+      e2 = hipGetLastError();
+      if (e2 != hipSuccess) return e2;
+      return hipEventRecord(R->done, s);
+    }
+    return hipGetLastError();
+  };
+  switch (p.D) {
+    case 128: return go(std::integral_constant<int, 128>{});
+    case 64: return go(std::integral_constant<int, 64>{});
+    default: return go(std::integral_constant<int, 72>{});
+  }
 }
 
 }  // namespace mxa

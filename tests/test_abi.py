@@ -176,3 +176,22 @@ def test_mfma_path_for_unaligned_strides():
         assert flash_attn_uses_mfma(base, base + 2, base + 6, base, p)
     p = AttnParams(Sq=100, Skv=300, Hq=4, Hkv=2, D=128)
     assert not flash_attn_uses_mfma(base + 1, base, base, base, p)
+
+
+def test_flash_split_plan():
+    """mx_flash_attn_split_plan on 256 CUs: grids of few units split by key range (up to
+    8 parts of >= 4 tiles); the config-2 grid (408 units, a last round of 152 on a
+    power-limited chip), whole rounds, causal calls and short key ranges run unsplit.
+    Host-side."""
+    from miroxen_amd.attention import flash_attn_split_plan
+    P = lambda Sq, Skv, H, D=128, c=0: AttnParams(Sq=Sq, Skv=Skv, Hq=H, Hkv=H, D=D, causal=c)
+    assert flash_attn_split_plan(P(4352, 4352, 24), 256) == (408, 0, 1)
+    assert flash_attn_split_plan(P(4096, 4096, 32), 256) == (512, 0, 1)
+    assert flash_attn_split_plan(P(1024, 8192, 8, c=1), 256) == (32, 0, 1)
+    assert flash_attn_split_plan(P(300, 300, 2), 256) == (4, 0, 1)
+    for shape in ((256, 2048, 2), (1000, 1000, 2), (4352, 4352, 6), (600, 2000, 6, 64), (1000, 1000, 4, 72)):
+        f, u, s = flash_attn_split_plan(P(shape[0], shape[1], shape[2], *shape[3:]), 256)
+        ntq = -(-shape[0] // 256)
+        assert f == 0 and u == ntq * shape[2] and 2 <= s <= 8 and s * 4 <= -(-shape[1] // 64), (shape, f, u, s)
+    # the plan depends on the CU count it is given: 1 CU runs every grid whole
+    assert flash_attn_split_plan(P(256, 2048, 2), 1) == (2, 0, 1)

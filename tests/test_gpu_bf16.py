@@ -281,3 +281,69 @@ def test_small_head_dim_fast_path(cuda, case):
     assert ok, f"max_abs={err} limit={tol} rel_rms={rr}"
     assert cosine(got, want) >= 0.9999 and max_abs(got, want) <= 2e-2
     _check_guards(buf, 16, Sq, Hq * D, Hq * D, rows)
+
+
+# Key-range split of the grid's last round (flash_attn_split_plan): the split units'
+# rows against the oracle, parts whose keys are all masked, GQA / D = 64 / 72 with
+# padded strides, and repeat / cross-stream calls sharing the library's split region.
+# Sq, Skv, Hq, Hkv, D, pad, dead_from (keys >= dead_from masked; 0: no mask)
+SPLIT = [
+    (1024, 1024, 2, 2, 128, 0, 700), (1000, 1000, 4, 2, 72, 5, 0), (600, 2000, 6, 3, 64, 8, 0),
+    (4352, 4352, 6, 6, 128, 0, 4296), (257, 4000, 3, 1, 128, 0, 1000),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT, ids=lambda c: "x".join(map(str, c[:5])) + f"_p{c[5]}d{c[6]}")
+def test_split_grid(cuda, case):
+    from miroxen_amd.attention import flash_attn_split_plan
+    Sq, Skv, Hq, Hkv, D, pad, dead = case
+    print(f"split case {case}", flush=True)
+    q, k, v, qs, ks, os_ = _make(Sq, Skv, Hq, Hkv, D, pad, 1.0, 55 + Sq + D, cuda)
+    mask = None
+    if dead:
+        mask = torch.ones(Skv, dtype=torch.uint8)
+        mask[dead:] = 0
+    p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=D, q_stride=qs if pad else 0, kv_stride=ks if pad else 0,
+                   o_stride=os_ if pad else 0, kv_valid=None if mask is None else mask.to(cuda))
+    full, units, parts = flash_attn_split_plan(p)
+    assert parts > 1 and units > 0, "case chosen to exercise the split"
+    out, buf = _run(flash_attn, q, k, v, p, Sq, os_)
+    # rows of split units: unit L = head * ntq + qtile, split units are L >= full
+    ntq = (Sq + 255) // 256
+    rows = sorted(set(query_rows(Sq, Hq)) | set(range(0, Sq, max(1, Sq // 53))) | {Sq - 1})
+    got = _f32(out[rows, : Hq * D])
+    want = oracle.attention_f64(_bits(q), _bits(k), _bits(v), Sq, Skv, Hq, Hkv, D, q_stride=qs, kv_stride=ks,
+                                kv_valid=None if mask is None else mask.numpy(),
+                                rows=np.array(rows, np.int32)).reshape(len(rows), -1)
+    ok, err, tol, rr = reference_gate(got, want)
+    assert ok, f"max_abs={err} limit={tol} rel_rms={rr}"
+    assert cosine(got, want) >= 0.9999 and max_abs(got, want) <= 2e-2
+    split_heads = sorted({L // ntq for L in range(full, full + units)})
+    cols = np.concatenate([np.arange(h * D, (h + 1) * D) for h in split_heads])
+    assert max_abs(got[:, cols], want[:, cols]) <= 2e-2
+    _check_guards(buf, 16, Sq, os_, Hq * D, rows)
+    # repeat: bit-identical
+    out2, _ = _run(flash_attn, q, k, v, p, Sq, os_)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+
+
+def test_split_calls_on_two_streams(cuda):
+    """Two split calls on different streams share the library's partial region; the
+    second waits for the first's merge, so both results equal their single-stream runs."""
+    S, H = 1024, 4
+    q1, k1, v1, *_ = _make(S, S, H, H, 128, 0, 1.0, 8, cuda)
+    q2, k2, v2, *_ = _make(S, S, H, H, 128, 0, 2.0, 9, cuda)
+    p = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128)
+    ref1, ref2 = torch.empty_like(q1), torch.empty_like(q2)
+    flash_attn(q1, k1, v1, ref1, p); flash_attn(q2, k2, v2, ref2, p)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    o1, o2 = torch.empty_like(q1), torch.empty_like(q2)
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            flash_attn(q1, k1, v1, o1, p, stream=s1)
+        with torch.cuda.stream(s2):
+            flash_attn(q2, k2, v2, o2, p, stream=s2)
+        torch.cuda.synchronize()
+        assert torch.equal(o1.view(torch.int16), ref1.view(torch.int16))
+        assert torch.equal(o2.view(torch.int16), ref2.view(torch.int16))
