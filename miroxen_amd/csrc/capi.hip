@@ -26,6 +26,8 @@ mx_sage_layout sage_layout(const mx_attn_params&);
 hipError_t launch_sage_quantize(const uint16_t*, const uint16_t*, const uint16_t*, const mx_attn_params&, char*,
                                 hipStream_t, const NormRope*, int q_group);
 hipError_t launch_sage_attend(uint16_t*, const mx_attn_params&, const char*, hipStream_t);
+hipError_t launch_sage_fp8(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, const mx_attn_params&, char*,
+                           hipStream_t);
 size_t mx_qscale_size(int64_t rows, int64_t K);
 hipError_t launch_mxfp8_quant(const uint16_t*, int64_t, int64_t, int64_t, uint8_t*, uint8_t*, hipStream_t);
 hipError_t launch_mxfp8_gemm(const uint8_t*, const uint8_t*, const uint8_t*, const uint8_t*, uint16_t*, int64_t, int,
@@ -261,12 +263,9 @@ int mx_flash_attn_fp8(const void* q, const void* k, const void* v, void* o, cons
   int rc = sage_args(q, k, v, o, p, ws, &a, &ok);
   if (rc) return rc;
   if (!ws || !ok) return mx_flash_attn(q, k, v, o, p, stream);  // reference :491
-  auto s = static_cast<hipStream_t>(stream);
-  rc = hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                                            static_cast<const uint16_t*>(v), a, static_cast<char*>(ws), s, nullptr, 16),
-                  "flash_attn_fp8 prologue");
-  if (rc) return rc;
-  return hip_status(mxa::launch_sage_attend(static_cast<uint16_t*>(o), a, static_cast<const char*>(ws), s),
+  return hip_status(mxa::launch_sage_fp8(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                         static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), a,
+                                         static_cast<char*>(ws), static_cast<hipStream_t>(stream)),
                     "flash_attn_fp8");
 }
 
@@ -288,12 +287,9 @@ int mx_flash_attn_fp8_noalloc(const void* q, const void* k, const void* v, void*
   if (rc) return rc;
   // the prologue rewrites every region the attention kernel reads and zeroes the
   // split arrival counters, so nothing is left over from the previous call
-  auto s = static_cast<hipStream_t>(stream);
-  rc = hip_status(mxa::launch_sage_quantize(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                                            static_cast<const uint16_t*>(v), a, static_cast<char*>(ws), s, nullptr, 16),
-                  "flash_attn_fp8_noalloc prologue");
-  if (rc) return rc;
-  return hip_status(mxa::launch_sage_attend(static_cast<uint16_t*>(o), a, static_cast<const char*>(ws), s),
+  return hip_status(mxa::launch_sage_fp8(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                         static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), a,
+                                         static_cast<char*>(ws), static_cast<hipStream_t>(stream)),
                     "flash_attn_fp8_noalloc");
 }
 

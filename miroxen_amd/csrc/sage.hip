@@ -790,10 +790,18 @@ sage_attn_gen(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, cons
 constexpr int kPipeMaxTiles = 512;  // tile table entries (8 KB of LDS): Skv <= 32768
 constexpr int kPipeWaves = 4;       // 128 queries per work-group, two work-groups per CU
 
+// QF: the kernel quantizes its own queries from bf16 q (qb; qi and qs are not read):
+// each 16-row group of a wave is quantized exactly as prep_stats_q<D, -1, 16> does it
+// (abs-max over the group's rows and channels, 127 / amax, rint), so the result equals
+// the prologue-quantized path bit for bit, and the prologue skips Q (its bf16 read and
+// int8 write). The queries of a unit are read by its work-groups before any of them
+// writes the unit's output, so o may still alias q.
+template <bool QF>
 __global__ void __launch_bounds__(256, 2)
 sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, const uint8_t* __restrict__ vt_g,
                const float* __restrict__ qs, const u32x4* __restrict__ tab_g, const float* __restrict__ va,
-               uint16_t* __restrict__ o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad, SageSplit sp) {
+               uint16_t* o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad, SageSplit sp,
+               const uint16_t* qb, float qmult) {
   constexpr int NW = kPipeWaves, QT = NW * 32, D = kPipeD;
   __shared__ __align__(16) unsigned char kring[4 * KTILEB];
   __shared__ __align__(16) unsigned char vring[4 * VTILEB];
@@ -844,6 +852,16 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
     buf2lds16(rv_r, lv, so, (MXA_LDS void*)d);
     buf2lds16(rv_r, lv, so + vstep, (MXA_LDS void*)(d + 1024));
   };
+  // QF: this lane's 64 bf16 channels of its row (h * 16 + cc * 32 + [0, 16); rows past
+  // Sq are 0), loaded before the tile DMA so the quantization below waits for them only
+  // (unconditional loads of a clamped row, zeroed afterwards: no per-lane branches)
+  u32x4 raw[8];
+  if constexpr (QF) {
+    const int rc = row < p.Sq ? row : p.Sq - 1;
+    const uint16_t* src = qb + int64_t(rc) * p.q_stride + int64_t(head) * D + h * 16;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) raw[j] = *reinterpret_cast<const u32x4*>(src + (j >> 1) * 32 + (j & 1) * 8);
+  }
   dma_k(tb, tb);
   dma_k(tb + 1, tb + 1);
   dma_k(tb + 2, tb + 2);
@@ -853,12 +871,37 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   dma_v(tb, tb + 3);  // stands in for V(tb - 1) (read with P(tb - 1) = 0): finite bytes
 
   i32x4 qf[4];
-  {
+  float qscale;
+  if constexpr (!QF) {
     const int8_t* src = qi + (int64_t(head) * sq_pad + row) * D + h * 16;
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) qf[cc] = *reinterpret_cast<const i32x4*>(src + cc * 32);
+    qscale = qs[int64_t(head) * (sq_pad / 16) + row / 16];
+  } else {
+    float x[8][8], am = 0.f;
+    const uint32_t keep = row < p.Sq ? ~0u : 0u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[j][e] = bf2f(uint16_t((raw[j][e >> 1] & keep) >> ((e & 1) * 16)));
+        am = fmaxf(am, fabsf(x[j][e]));
+      }
+    // the 16-row group of this lane: lanes with the same n >> 4 in both wave halves
+    // (DPP row rotations within each 16-lane row: no LDS round trips)
+    am = fmaxf(am, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(am), 0x128, 0xf, 0xf, false)));
+    am = fmaxf(am, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(am), 0x124, 0xf, 0xf, false)));
+    am = fmaxf(am, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(am), 0x122, 0xf, 0xf, false)));
+    am = fmaxf(am, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(am), 0x121, 0xf, 0xf, false)));
+    am = fmaxf(am, other_half(am));
+    const float inv = am > 0.f ? 127.f / am : 0.f;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const u32x2 lo = quant8(x[2 * cc], inv), hi = quant8(x[2 * cc + 1], inv);
+      qf[cc] = i32x4{int(lo[0]), int(lo[1]), int(hi[0]), int(hi[1])};
+    }
+    qscale = am / 127.f * qmult;
   }
-  const float qscale = qs[int64_t(head) * (sq_pad / 16) + row / 16];
   // tile table (liveness bits, K scale; written by the prologue's prep_kv_quant): one
   // coalesced 16-byte load per lane; the entry past the last tile is read by the last
   // iteration (its result is unused)
@@ -1076,14 +1119,15 @@ mx_sage_layout sage_layout(const mx_attn_params& p) {
 // (D == 128 and nr128_supported, checked by the caller).
 template <int D>
 hipError_t sage_quantize_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, const mx_attn_params& p,
-                           char* ws, hipStream_t s, const NormRope* nr, int q_group) {
+                           char* ws, hipStream_t s, const NormRope* nr, int q_group, bool skip_q) {
   const mx_sage_layout L = sage_layout(p);
   const int nb = (p.Skv + kStatTok - 1) / kStatTok;
   float* part = reinterpret_cast<float*>(ws + L.part);
   float* km = reinterpret_cast<float*>(ws + L.km);
   float* va = reinterpret_cast<float*>(ws + L.va);
   const int64_t qgroups = int64_t(p.Hq) * (L.sq_pad / 16);
-  const int64_t blocks1 = int64_t(p.Hkv) * nb + (qgroups + 3) / 4;
+  // skip_q: the attention kernel quantizes Q itself (sage_attn_pipe<true>)
+  const int64_t blocks1 = int64_t(p.Hkv) * nb + (skip_q ? 0 : (qgroups + 3) / 4);
   if (blocks1 > 0x7fffffff) return hipErrorInvalidValue;
   const float qmult = p.scale * kLog2e;
   const NormRope none{};
@@ -1123,12 +1167,13 @@ hipError_t sage_quantize_d(const uint16_t* q, const uint16_t* k, const uint16_t*
 
 hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint16_t* v, const mx_attn_params& p,
                                 char* ws, hipStream_t s, const NormRope* nr, int q_group) {
-  if (p.D == 128) return sage_quantize_d<128>(q, k, v, p, ws, s, nr, q_group);
-  if (p.D == 64) return sage_quantize_d<64>(q, k, v, p, ws, s, nr, q_group);
+  if (p.D == 128) return sage_quantize_d<128>(q, k, v, p, ws, s, nr, q_group, false);
+  if (p.D == 64) return sage_quantize_d<64>(q, k, v, p, ws, s, nr, q_group, false);
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_sage_attend(uint16_t* o, const mx_attn_params& p, const char* ws, hipStream_t s) {
+hipError_t sage_attend_impl(uint16_t* o, const mx_attn_params& p, const char* ws, hipStream_t s,
+                            const uint16_t* qb) {
   static_assert(kSqPad % 256 == 0 && kSqPad % (kPipeWaves * 32) == 0, "Q padding must cover whole query tiles");
   const mx_sage_layout L = sage_layout(p);
   const SageShape sh = sage_shape(p);
@@ -1144,9 +1189,13 @@ hipError_t launch_sage_attend(uint16_t* o, const mx_attn_params& p, const char* 
   const auto vt = reinterpret_cast<const uint8_t*>(ws + L.vt);
   const auto qs = reinterpret_cast<const float*>(ws + L.qs);
   const auto va = reinterpret_cast<const float*>(ws + L.va);
-  if (sh.pipe)
-    hipLaunchKernelGGL(sage_attn_pipe, dim3(unsigned(blocks)), dim3(sh.nw * 64), 0, s, qi, ki, vt, qs,
-                       reinterpret_cast<const u32x4*>(ws + L.tab), va, o, p, L.sq_pad, L.skv_pad, sp);
+  const float qmult = p.scale * kLog2e;
+  if (sh.pipe && qb)
+    hipLaunchKernelGGL(sage_attn_pipe<true>, dim3(unsigned(blocks)), dim3(sh.nw * 64), 0, s, qi, ki, vt, qs,
+                       reinterpret_cast<const u32x4*>(ws + L.tab), va, o, p, L.sq_pad, L.skv_pad, sp, qb, qmult);
+  else if (sh.pipe)
+    hipLaunchKernelGGL(sage_attn_pipe<false>, dim3(unsigned(blocks)), dim3(sh.nw * 64), 0, s, qi, ki, vt, qs,
+                       reinterpret_cast<const u32x4*>(ws + L.tab), va, o, p, L.sq_pad, L.skv_pad, sp, qb, qmult);
   else if (p.D == 128)
     hipLaunchKernelGGL((sage_attn_gen<128, kSageStages>), dim3(unsigned(blocks)), dim3(sh.nw * 64), 0, s, qi, ki, vt,
                        qs, reinterpret_cast<const float*>(ws + L.ks), va, o, p, L.sq_pad, L.skv_pad, sp);
@@ -1156,6 +1205,23 @@ hipError_t launch_sage_attend(uint16_t* o, const mx_attn_params& p, const char* 
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
+}
+
+hipError_t launch_sage_attend(uint16_t* o, const mx_attn_params& p, const char* ws, hipStream_t s) {
+  return sage_attend_impl(o, p, ws, s, nullptr);
+}
+
+// The whole quantized call (plain prologue, Q per 16 tokens): on the D = 128 pipe
+// kernel the attention kernel quantizes Q itself and the prologue reads only K and V;
+// otherwise the prologue quantizes Q into the workspace.
+hipError_t launch_sage_fp8(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
+                           const mx_attn_params& p, char* ws, hipStream_t s) {
+  const bool fuse_q = sage_shape(p).pipe;
+  hipError_t e = p.D == 128 ? sage_quantize_d<128>(q, k, v, p, ws, s, nullptr, 16, fuse_q)
+               : p.D == 64  ? sage_quantize_d<64>(q, k, v, p, ws, s, nullptr, 16, false)
+                            : hipErrorInvalidValue;
+  if (e != hipSuccess) return e;
+  return sage_attend_impl(o, p, ws, s, fuse_q ? q : nullptr);
 }
 
 }  // namespace mxa

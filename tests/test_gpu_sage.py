@@ -173,9 +173,14 @@ def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
     ws = _ws(p, cuda)
     o = torch.empty_like(q)
     flash_attn_fp8(q, k, v, o, p, ws)
+    # the quantized operands the emulator is fed: flash_attn_fp8 quantizes Q inside the
+    # attention kernel (the workspace holds no Q), bit-identical to the prologue's Q
+    # (test_fused_q_equals_prologue_q), which sage_quantize writes
+    wsq = _ws(p, cuda)
+    sage_quantize(q, k, v, p, wsq)
     torch.cuda.synchronize()
     L = sage_layout(p)
-    g = _quantized(ws, p, L)
+    g = _quantized(wsq, p, L)
     rows = np.array(rows, np.int32)
     mk = None if mask is None else mask.cpu().numpy()
     # the kernel balances its grid by splitting the last round's units by key range;
@@ -386,3 +391,40 @@ def test_sage_d64(cuda, Sq, Skv, Hq, Hkv, pad, kbias, masked):
           f"relrms(reference rule)={rr_ref:.4f}", flush=True)
     assert c_emu >= 0.99999 and e_emu <= max(2e-2, 2.0 ** -4 * np.abs(emu).max())  # as _sage_vs_oracle
     assert c_ex >= 0.995 and rr < max(0.04, rr_ref + 0.0025)
+
+
+# flash_attn_fp8 on the D = 128 pipe kernel quantizes Q inside the attention kernel
+# (the prologue skips it); sage_quantize + sage_attend quantize Q in the prologue.
+# Both must give the same output bit for bit: ragged and padded query rows, GQA,
+# masks, a negative-free scale other than the default, split grids, config 3.
+# Sq, Skv, Hq, Hkv, pad, kbias, scale, masked
+FUSED_Q = [
+    (1, 64, 1, 1, 0, 1.0, 0.0, False), (77, 300, 4, 2, 5, 2.0, 0.0, True), (1000, 1117, 6, 3, 8, 4.0, 0.3, False),
+    (2047, 2047, 4, 4, 0, 1.0, 0.0, True), (4352, 4352, 24, 24, 0, 2.0, 0.0, True),
+]
+
+
+@pytest.mark.parametrize("case", FUSED_Q, ids=lambda c: "x".join(map(str, c[:4])) + f"_p{c[4]}{'_m' if c[7] else ''}")
+def test_fused_q_equals_prologue_q(cuda, case):
+    Sq, Skv, Hq, Hkv, pad, kbias, scale, masked = case
+    print(f"fused-Q case {case}", flush=True)
+    q, k, v, qs, ks = _bias_inputs(Sq, Skv, Hq, Hkv, 128, pad, kbias, cuda, 31 + Sq)
+    mask = None
+    if masked:
+        mask = (torch.rand(Skv, generator=torch.Generator().manual_seed(Skv)) > 0.1).to(torch.uint8).to(cuda)
+    p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=128, scale=scale, q_stride=qs if pad else 0,
+                   kv_stride=ks if pad else 0, kv_valid=mask)
+    assert flash_attn_fp8_ok(q, k, v, q, p)
+    ws1, ws2 = _ws(p, cuda), _ws(p, cuda)
+    o1 = torch.full((Sq, Hq * 128), 3.0, dtype=torch.bfloat16, device=cuda)
+    o2 = torch.full((Sq, Hq * 128), 5.0, dtype=torch.bfloat16, device=cuda)
+    flash_attn_fp8(q, k, v, o1, p, ws1)
+    sage_quantize(q, k, v, p, ws2)
+    sage_attend(o2, p, ws2)
+    torch.cuda.synchronize()
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    # K / V regions of the two workspaces agree as well (the prologue's K/V part is shared)
+    L = sage_layout(p)
+    a, b = _quantized(ws1, p, L), _quantized(ws2, p, L)
+    for name in ("ki", "vt", "ks", "km", "va"):
+        assert np.array_equal(a[name], b[name]), name
