@@ -214,11 +214,14 @@ def _only(which: str, n: int) -> int:
         return 0
     if which == "sage":
         sage_quantize(q, k, v, p, ws)
+    from miroxen_amd import flash_attn_fp8
     for _ in range(n):
         if which == "bf16":
             flash_attn(q, k, v, o, p)
         elif which == "sage":
             sage_attend(o, p, ws)
+        elif which == "sage_e2e":  # the product path: K/V prologue + attention quantizing Q
+            flash_attn_fp8(q, k, v, o, p, ws)
         else:
             sage_quantize(q, k, v, p, ws)
     torch.cuda.synchronize()
@@ -235,7 +238,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--skip-large", action="store_true", help="skip configs 4 and 5 (S=12544, S=32760)")
     ap.add_argument("--no-blockscale", action="store_true", help="skip the MXFP8 block-scaled GEMM leg")
-    ap.add_argument("--only", choices=["bf16", "sage", "prologue", "fused", "copy", "blockscale"],
+    ap.add_argument("--only", choices=["bf16", "sage", "sage_e2e", "prologue", "fused", "copy", "blockscale"],
                     help="profiling driver: run just this kernel --steps times (no warm-up, no JSON); "
                          "'copy' is a 256 MiB device copy for calibrating HBM byte counters")
     args = ap.parse_args()
