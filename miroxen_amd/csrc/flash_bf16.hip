@@ -390,8 +390,16 @@ __device__ __forceinline__ void store_partial(const QBlock<DH>& X, const BfSplit
   sp.ml[blk * 256 + lrow] = f32x4{X.m, X.l, __builtin_ldexpf(1.f, e - 15), 0.f};
 }
 
+// Occupancy: one work-group of 8 waves per CU, two waves per SIMD. The causal kernels
+// state that target (waves_per_eu 2): aiming for three waves per SIMD, the compiler caps
+// a kernel at 168 VGPRs, and the causal tile loop needs 177 (the per-lane diagonal
+// mask), so it gave up the LDS operand prefetch (one operand register set, each read
+// waited for before its MFMA; config-2 shape 176 -> 146 us with the target stated).
+// The non-causal kernels keep the equivalent of __launch_bounds__(512, 1): the stated
+// target changes their schedule for the worse at D = 64 and not at all at D = 128.
 template <int DH, bool CAUSAL, bool SPLIT>
-__global__ void __launch_bounds__(512, 1)
+__global__ void __attribute__((amdgpu_flat_work_group_size(CAUSAL ? 512 : 1, 512),
+                               amdgpu_waves_per_eu(CAUSAL ? 2 : 1, CAUSAL ? 2 : 8)))
 flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
               uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign, BfSplit sp) {
   using Dm = Dims<DH>;
