@@ -74,39 +74,24 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
     const int64_t t0 = int64_t(b) * kStatTok;
     const int64_t t1 = t0 + kStatTok < p.Skv ? t0 + kStatTok : p.Skv;
     float sum = 0.f, am = 0.f;
-    for (int64_t c0 = t0; c0 < t1; c0 += kStatChunk) {
-      const int rows = int(t1 - c0 < kStatChunk ? t1 - c0 : kStatChunk);
-      if constexpr (NRM >= 0) {
-        // K rows normalised on the way into LDS: one row per 16 lanes, 16 per pass
-        // (all eight rows of a lane group loaded before any is normalised)
-        const int lane = tid & 63, c = (lane & 15) * 8;
-        constexpr int RPG = kStatChunk / 16;  // rows per 16-lane group
-        u32x4 raw[RPG];
-#pragma unroll
-        for (int u = 0; u < RPG; ++u) {
-          const int r = u * 16 + (tid >> 4);
-          raw[u] = u32x4{0, 0, 0, 0};
-          if (r < rows) raw[u] = *reinterpret_cast<const u32x4*>(k + (c0 + r) * p.kv_stride + int64_t(h) * D + c);
-        }
-#pragma unroll
-        for (int u = 0; u < RPG; ++u) {
-          const int r = u * 16 + (tid >> 4);
-          float x[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) x[j] = bf2f(uint16_t(raw[u][j >> 1] >> ((j & 1) * 16)));
-          nr128_row<NRM>(x, c0 + r, r < rows, nk, lane);
-          if (r < rows) *reinterpret_cast<u32x4*>(&kt[r * D + c]) = pack8_bf16(x);
-        }
-        for (int i = tid; i < rows * (D / 8); i += 256) {
-          const int r = i / (D / 8), cc = (i % (D / 8)) * 8;
-          *reinterpret_cast<u32x4*>(&vt_[r * D + cc]) =
-              *reinterpret_cast<const u32x4*>(v + (c0 + r) * p.kv_stride + int64_t(h) * D + cc);
-        }
-      } else {
-        // every load of the chunk in flight before the first LDS store (rows past the
-        // chunk's end are not loaded; their LDS rows are never summed)
-        constexpr int NL = kStatChunk * (D / 8) / 256;
-        u32x4 kr[NL], vr[NL];
+    // sequential per-channel sum (K, token order) / abs-max (V) of the chunk staged in LDS
+    auto fold = [&](int rows) __attribute__((always_inline)) {
+      if (tid < D) {
+#pragma unroll 16
+        for (int r = 0; r < rows; ++r) sum += bf2f(kt[r * D + tid]);  // sequential, token order
+      } else if (tid < 2 * D) {
+        const int d = tid - D;
+#pragma unroll 16
+        for (int r = 0; r < rows; ++r) am = fmaxf(am, fabsf(bf2f(vt_[r * D + d])));
+      }
+    };
+    if constexpr (NRM < 0) {
+      // every load of a chunk in flight before the first LDS store, and the next chunk's
+      // loads in flight while this one is folded (rows past a chunk's end are not
+      // loaded; their LDS rows are never read)
+      constexpr int NL = kStatChunk * (D / 8) / 256;
+      u32x4 kr[NL], vr[NL];
+      auto load = [&](int64_t c0, int rows) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < NL; ++u) {
           const int i = tid + 256 * u, r = i / (D / 8), c = (i % (D / 8)) * 8;
@@ -117,23 +102,58 @@ __global__ void __launch_bounds__(256) prep_stats_q(const uint16_t* __restrict__
             vr[u] = *reinterpret_cast<const u32x4*>(v + g);
           }
         }
+      };
+      const int nch = int((t1 - t0 + kStatChunk - 1) / kStatChunk);  // 1 or 2
+      load(t0, int(t1 - t0 < kStatChunk ? t1 - t0 : kStatChunk));
+      for (int ch = 0; ch < nch; ++ch) {
+        const int64_t c0 = t0 + int64_t(ch) * kStatChunk;
+        const int rows = int(t1 - c0 < kStatChunk ? t1 - c0 : kStatChunk);
 #pragma unroll
         for (int u = 0; u < NL; ++u) {
           const int i = tid + 256 * u, r = i / (D / 8), c = (i % (D / 8)) * 8;
           *reinterpret_cast<u32x4*>(&kt[r * D + c]) = kr[u];
           *reinterpret_cast<u32x4*>(&vt_[r * D + c]) = vr[u];
         }
+        __syncthreads();
+        if (ch + 1 < nch) load(c0 + kStatChunk, int(t1 - c0 - kStatChunk < kStatChunk ? t1 - c0 - kStatChunk
+                                                                                       : kStatChunk));
+        fold(rows);
+        __syncthreads();
       }
-      __syncthreads();
-      if (tid < D) {
-#pragma unroll 16
-        for (int r = 0; r < rows; ++r) sum += bf2f(kt[r * D + tid]);  // sequential, token order
-      } else if (tid < 2 * D) {
-        const int d = tid - D;
-#pragma unroll 16
-        for (int r = 0; r < rows; ++r) am = fmaxf(am, fabsf(bf2f(vt_[r * D + d])));
+    } else {
+      for (int64_t c0 = t0; c0 < t1; c0 += kStatChunk) {
+        const int rows = int(t1 - c0 < kStatChunk ? t1 - c0 : kStatChunk);
+        {
+          // K rows normalised on the way into LDS: one row per 16 lanes, 16 per pass
+          // (all eight rows of a lane group loaded before any is normalised)
+          const int lane = tid & 63, c = (lane & 15) * 8;
+          constexpr int RPG = kStatChunk / 16;  // rows per 16-lane group
+          u32x4 raw[RPG];
+#pragma unroll
+          for (int u = 0; u < RPG; ++u) {
+            const int r = u * 16 + (tid >> 4);
+            raw[u] = u32x4{0, 0, 0, 0};
+            if (r < rows) raw[u] = *reinterpret_cast<const u32x4*>(k + (c0 + r) * p.kv_stride + int64_t(h) * D + c);
+          }
+#pragma unroll
+          for (int u = 0; u < RPG; ++u) {
+            const int r = u * 16 + (tid >> 4);
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = bf2f(uint16_t(raw[u][j >> 1] >> ((j & 1) * 16)));
+            nr128_row<NRM>(x, c0 + r, r < rows, nk, lane);
+            if (r < rows) *reinterpret_cast<u32x4*>(&kt[r * D + c]) = pack8_bf16(x);
+          }
+          for (int i = tid; i < rows * (D / 8); i += 256) {
+            const int r = i / (D / 8), cc = (i % (D / 8)) * 8;
+            *reinterpret_cast<u32x4*>(&vt_[r * D + cc]) =
+                *reinterpret_cast<const u32x4*>(v + (c0 + r) * p.kv_stride + int64_t(h) * D + cc);
+          }
+        }
+        __syncthreads();
+        fold(rows);
+        __syncthreads();
       }
-      __syncthreads();
     }
     if (tid < D) part[(int64_t(h) * nb + b) * D + tid] = sum / float(p.Skv);
     else if (tid < 2 * D) part[int64_t(p.Hkv) * nb * D + (int64_t(h) * nb + b) * D + (tid - D)] = am;
