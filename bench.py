@@ -360,6 +360,9 @@ def main() -> int:
             n = max(3, args.steps // 20)
             mb = _time(lambda: flash_attn(qc, kc, vc, oc, pc), n, args.warmup, args.warm_seconds)
             me = _time(lambda: flash_attn_fp8(qc, kc, vc, oc, pc, wc), n, args.warmup, args.warm_seconds)
+            # kernel-only: sage_attend reads the prologue's int8 Q, which flash_attn_fp8 (its
+            # attention kernel quantizes Q itself) does not write
+            sage_quantize(qc, kc, vc, pc, wc)
             mk = _time(lambda: sage_attend(oc, pc, wc), n, args.warmup, args.warm_seconds)
             others[f"config{cid}"] = {
                 "workload": c.name, "H": c.H, "S": c.S, "steps": n,

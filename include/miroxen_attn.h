@@ -68,7 +68,8 @@ int mx_flash_attn_fp8_ok(const void* q, const void* k, const void* v, const void
  * the per-channel K mean), V -> OCP e4m3 per channel, INT8 QK^T and FP8 PV MFMA,
  * fp32 accumulation. ws: >= mx_flash_attn_fp8_workspace(p) bytes, 256-byte aligned.
  * Falls back to mx_flash_attn when ws == NULL or flash_attn_fp8_ok is false.
- * o may alias q (the main kernel reads only the workspace). */
+ * o may alias q (at D = 128 the attention kernel reads each unit's Q rows before any
+ * of that unit's output is written; otherwise it reads only the workspace). */
 int mx_flash_attn_fp8(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
                       void* ws, void* stream);
 
@@ -142,7 +143,10 @@ int mx_sage_quantize(const void* q, const void* k, const void* v, const mx_attn_
 int mx_sage_quantize_qgroup(const void* q, const void* k, const void* v, const mx_attn_params* p, void* ws,
                             int q_group, void* stream);
 
-/* Main kernel only, on a workspace already filled by mx_sage_quantize. */
+/* Main kernel only, on a workspace already filled by mx_sage_quantize (or
+ * mx_sage_quantize_qgroup / mx_sage_quantize_norm_rope). A workspace last used by
+ * mx_flash_attn_fp8 is not enough: at D = 128 that call quantizes Q inside its attention
+ * kernel and leaves the workspace's Q regions unwritten. */
 int mx_sage_attend(void* o, const mx_attn_params* p, const void* ws, void* stream);
 
 /* Message of this thread's last failed call ("" if none). */
