@@ -347,3 +347,47 @@ def test_split_calls_on_two_streams(cuda):
         torch.cuda.synchronize()
         assert torch.equal(o1.view(torch.int16), ref1.view(torch.int16))
         assert torch.equal(o2.view(torch.int16), ref2.view(torch.int16))
+
+
+def test_graph_capture_replays(cuda):
+    """flash_attn and flash_attn_fp8 captured into a HIP graph (torch.cuda.graph) and
+    replayed with eager work in between: every replay equals the first bit for bit and
+    the eager result to the BF16 tolerance. Under capture flash_attn does not split its
+    grid (no library allocation or cross-stream event inside a graph)."""
+    from miroxen_amd import flash_attn_fp8, flash_attn_fp8_workspace
+    from miroxen_amd.attention import flash_attn_split_plan
+    S, H = 1024, 2
+    q, k, v, *_ = _make(S, S, H, H, 128, 0, 1.0, 61, cuda)
+    p = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=128)
+    assert flash_attn_split_plan(p)[2] > 1  # eager calls of this shape split
+    eager, eager8 = torch.empty_like(q), torch.empty_like(q)
+    ws = torch.zeros(flash_attn_fp8_workspace(p), dtype=torch.uint8, device=cuda)
+    flash_attn(q, k, v, eager, p)
+    flash_attn_fp8(q, k, v, eager8, p, ws)
+    torch.cuda.synchronize()
+    o, o8 = torch.empty_like(q), torch.empty_like(q)
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on the capture stream, as torch recommends
+        flash_attn(q, k, v, o, p)
+        flash_attn_fp8(q, k, v, o8, p, ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        flash_attn(q, k, v, o, p)
+        flash_attn_fp8(q, k, v, o8, p, ws)
+    outs = []
+    for i in range(3):
+        o.fill_(0); o8.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        outs.append((o.clone(), o8.clone()))
+        flash_attn(q, k, v, eager, p)  # eager work between replays (uses the split region)
+        torch.cuda.synchronize()
+    for a, b in outs[1:]:
+        assert torch.equal(a.view(torch.int16), outs[0][0].view(torch.int16))
+        assert torch.equal(b.view(torch.int16), outs[0][1].view(torch.int16))
+    assert max_abs(_f32(outs[0][0]), _f32(eager)) <= 4e-3
+    assert cosine(_f32(outs[0][0]), _f32(eager)) > 0.99999
+    assert torch.equal(outs[0][1].view(torch.int16), eager8.view(torch.int16))
