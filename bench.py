@@ -371,6 +371,32 @@ def main() -> int:
                 "sage_tflops_kernel": round(fc / (mk * 1e-3) / 1e12, 1)}
             del qc, kc, vc, oc, wc
 
+    # ---- BF16 beyond the BASELINE configs: causal at config 2's shape (useful FLOP =
+    # half the nominal), and grids of few units, where flash_attn splits the key range ----
+    extras = {}
+    if not args.skip_large:
+        g = torch.Generator(device=dev).manual_seed(77)
+        qx = torch.randn(S, H * D, device=dev, generator=g).to(torch.bfloat16)
+        kx = torch.randn(S, H * D, device=dev, generator=g).to(torch.bfloat16)
+        vx = torch.randn(S, H * D, device=dev, generator=g).to(torch.bfloat16)
+        ox = torch.empty_like(qx)
+        pcz = AttnParams(Sq=S, Skv=S, Hq=H, Hkv=H, D=D, causal=1)
+        mc = _time(lambda: flash_attn(qx, kx, vx, ox, pcz), 50, args.warmup, args.warm_seconds)
+        extras["bf16_causal_config2_shape"] = {"ms": round(mc, 4),
+                                               "tflops_useful": round(flop / 2 / (mc * 1e-3) / 1e12, 1)}
+        from miroxen_amd.attention import flash_attn_split_plan
+        small = {}
+        for sq, hh, skv in ((256, 2, 2048), (512, 4, 4096), (1024, 8, 8192)):
+            qs_ = torch.randn(sq, hh * D, device=dev, generator=g).to(torch.bfloat16)
+            ks_ = torch.randn(skv, hh * D, device=dev, generator=g).to(torch.bfloat16)
+            vs_ = torch.randn(skv, hh * D, device=dev, generator=g).to(torch.bfloat16)
+            os_ = torch.empty_like(qs_)
+            ps = AttnParams(Sq=sq, Skv=skv, Hq=hh, Hkv=hh, D=D)
+            msm = _time(lambda: flash_attn(qs_, ks_, vs_, os_, ps), 50, args.warmup, 0.1)
+            small[f"{sq}x{hh}x{skv}"] = {"ms": round(msm, 4), "split_plan": list(flash_attn_split_plan(ps))}
+        extras["bf16_small_grids"] = small
+        del qx, kx, vx, ox
+
     bs = None if args.no_blockscale else blockscale_leg(dev, args.steps, args.warmup, args.warm_seconds)
     if bs is not None and not args.no_cpu:
         bs["cpu_baseline"] = blockscale_cpu_baseline()
@@ -389,6 +415,7 @@ def main() -> int:
                      "frac": round(tflops / PEAK_BF16, 4), "traffic": traffic},
         "sage": sage,
         "other_configs": others,
+        "extras": extras,
         "blockscale": bs,
         "timed_wall_s": round(wall, 3),
     }
