@@ -25,9 +25,12 @@
  *    restatement of the reference's shuffle pattern.
  *  - or_f32_to_f16 / or_f16_to_f32: pinned against numpy's IEEE float16 cast
  *    (ties to even, subnormals, overflow) on hand cases and random values.
- *  - or_sage_emulate: pinned by its limit: with exact (unquantized) P/V it must
- *    equal or_attention_f64 to fp32 accuracy, and by the reference gate
- *    (rel-RMS < 4 % vs exact attention, tests/attention_fp8_test.cpp:65).
+ *  - or_sage_emulate: pinned by closed forms on hand-built quantized operands
+ *    (exact integer scores, power-of-two scales): two live keys whose second weight
+ *    448 * 2^-H * 2^-g is not an e4m3 value (P rounded in acc, l over the unrounded
+ *    weight, the 448 scale), a cross-tile rescale (alpha on l and acc) under the
+ *    reference rule and the lazy rule, one live key, uniform scores; and by the
+ *    reference gate (rel-RMS < 4 % vs exact attention, tests/attention_fp8_test.cpp:65).
  *  - or_mxfp8_quantize: pinned by the scale rule checked against float64
  *    ceil(log2(bmax / 448)) (independent of the frexp formulation), hand cases
  *    (zero block, bmax / 448 a power of two, just above one), exact round trips

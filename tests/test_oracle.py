@@ -296,6 +296,92 @@ def test_sage_lazy_max_headroom_matches_reference_rule():
     assert cosine(lazy, exact_rule) > 0.999
 
 
+def _sage_hand_inputs(scores, D=128, seed=21):
+    """Quantized Sage operands built by hand so every score is known exactly: one query
+    row whose int8 vector is all ones, keys whose channels sum to the integer score (the
+    int32 dot product is that integer), Q scale 2^-11 and K scales 1, random e4m3 V codes
+    (no NaN code) and per-channel V scales. scores: {key: score in units of 1/16 log2};
+    every other key is dead (masked). Returns the emulator's arguments, the mask and
+    the dequantized V rows.
+
+    Why sc = 2^-11: the reference's exponent (attention_fp8.cu:331, :337) is one FMA
+    with nm = (log2 448 - H - m) - 12582912 sc rounded to a float of magnitude
+    12582912 sc = 6144, whose ulp is 2^-11; so every weight carries a relative error
+    of at most 2^(2^-12) - 1 = 1.7e-4 and the closed forms hold to 5e-4."""
+    rng = np.random.default_rng(seed)
+    Skv = (max(scores) // 64 + 1) * 64
+    qi = np.zeros((1, 256, D), np.int8); qi[0, 0, :] = 1
+    ki = np.zeros((1, Skv, D), np.int8)
+    mask = np.zeros(Skv, np.uint8)
+    for key, s16 in scores.items():
+        s = s16 * 128  # x = s * 2^-11 = s16 / 16
+        ki[0, key, :] = s // D
+        ki[0, key, : s % D] += 1
+        assert int(ki[0, key].astype(np.int64).sum()) == s
+        mask[key] = 1
+    qs = np.full((1, 16), 2.0 ** -11, np.float32)
+    ks = np.ones((1, Skv // 64), np.float32)
+    codes = rng.integers(0, 0x7E, (1, D, Skv)) | (rng.integers(0, 2, (1, D, Skv)) << 7)
+    vt = codes.astype(np.uint8)
+    va = rng.uniform(0.5, 2.0, (1, D)).astype(np.float32)
+    table = _e4m3_table()
+    vhat = {key: np.array([table[int(c)] for c in vt[0, :, key]]) for key in scores}
+    args = (qi, ki, vt, qs, ks, va, 1, Skv, 1, 1, D)
+    return args, mask, vhat, va[0].astype(np.float64)
+
+
+@pytest.mark.parametrize("headroom,p_live2", [(0.0, 352.0), (3.0, 44.0)])
+def test_sage_two_live_keys_closed_form(headroom, p_live2):
+    """Two live keys in one tile, scores 10 and 5 (x = s / 16, gap 5/16 in log2 units).
+    The running max is the larger score, so P_0 = 448 * 2^-H exactly and the second
+    weight is f = 448 * 2^-H * 2^-(5/16) = 360.73 (H = 0) or 45.09 (H = 3), which is not
+    an e4m3 value: P_1 = e4m3(f) = 352 or 44 (hand-rounded from the OCP grid). The
+    reference accumulates rounded P into O (attention_fp8.cu:352) but sums the
+    UNROUNDED f into l (:339, :345) and divides by 448 l in the epilogue (:405-416):
+        out[d] = (P_0 v0[d] + P_1 v1[d]) * va[d] / (448 (P_0 + f)).
+    A wrong 448 constant, l over rounded P or P left unrounded all miss this by > 1 %."""
+    args, mask, vhat, va = _sage_hand_inputs({3: 10, 40: 5})
+    out = oracle.sage_emulate(*args, kv_valid=mask, headroom=headroom)[0, 0]
+    p0 = 448.0 * 2.0 ** -headroom
+    f1 = p0 * 2.0 ** (-5 / 16)
+    assert abs(f1 - p_live2) > 1.0  # the second weight really is rounded
+    want = (p0 * vhat[3] + p_live2 * vhat[40]) * va / (448.0 * (p0 + f1))
+    np.testing.assert_allclose(out, want, rtol=5e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("headroom,gap16,rescaled,p_b", [
+    (0.0, 40, True, 448.0),    # reference rule: any larger tile max moves m
+    (3.0, 56, True, 56.0),     # lazy rule: gap 3.5 > H moves m
+    (3.0, 40, False, 320.0),   # lazy rule: gap 2.5 <= H keeps m, P_b = e4m3(56 * 2^2.5)
+])
+def test_sage_cross_tile_rescale_closed_form(headroom, gap16, rescaled, p_b):
+    """Key 0 (tile 0, score 16) and key 64 (tile 1, score 16 + gap16): x_b - x_a = g =
+    gap16 / 16 in log2 units. Tile 0 sets m = x_a, P_a = 448 * 2^-H, l = P_a, acc = P_a v_a.
+    Tile 1 (attention_fp8.cu:322-353): when m moves to x_b, alpha = 2^-g rescales l and
+    acc (:328, :345, :347-353) and P_b = 448 * 2^-H; when the lazy rule keeps m, alpha = 1
+    and f_b = 448 * 2^-H * 2^g, rounded to e4m3 in acc but not in l:
+        out[d] = (alpha P_a v_a[d] + P_b v_b[d]) * va[d] / (448 (alpha P_a + f_b))."""
+    args, mask, vhat, va = _sage_hand_inputs({0: 16, 64: 16 + gap16})
+    out = oracle.sage_emulate(*args, kv_valid=mask, headroom=headroom)[0, 0]
+    g = gap16 / 16
+    pa = 448.0 * 2.0 ** -headroom
+    if rescaled:
+        alpha, fb = 2.0 ** -g, pa
+    else:
+        alpha, fb = 1.0, pa * 2.0 ** g
+        assert abs(fb - p_b) > 1.0
+    want = (alpha * pa * vhat[0] + p_b * vhat[64]) * va / (448.0 * (alpha * pa + fb))
+    np.testing.assert_allclose(out, want, rtol=5e-4, atol=1e-6)
+    # the same keys in the opposite tile order never rescale: P of the later, smaller
+    # key is e4m3(448 * 2^-H * 2^-g), l gets the unrounded weight
+    args, mask, vhat, va = _sage_hand_inputs({0: 16 + gap16, 64: 16})
+    out = oracle.sage_emulate(*args, kv_valid=mask, headroom=headroom)[0, 0]
+    f_small = pa * 2.0 ** -g
+    p_small = _e4m3_table()[oracle.e4m3(np.float32(f_small))]
+    want = (pa * vhat[0] + p_small * vhat[64]) * va / (448.0 * (pa + f_small))
+    np.testing.assert_allclose(out, want, rtol=5e-4, atol=1e-6)
+
+
 # ---------------- head_norm_rope (reference src/kernels/ops.cu:87-119) ----------------
 
 def _nr_inputs(S, H, D, seed, stride_extra=0, col0=0):
