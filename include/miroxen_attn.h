@@ -46,7 +46,14 @@ typedef struct mx_attn_params {
 
 /* Reference: mx::flash_attn, src/kernels/attention.h:21-22 (impl attention.cu:409-417).
  * D in {64,72,128}; bf16 in, fp32 accumulate, bf16 out. Invalid arguments ->
- * MX_E_INVALID with the reference's validate() rules (attention.cu:350-369). */
+ * MX_E_INVALID with the reference's validate() rules (attention.cu:350-369).
+ * Stream-ordered, no allocation, no host sync. Grids of few units (the last round
+ * leaves most CUs idle, see mx_flash_attn_split_plan) run split into key ranges whose
+ * partials live in a fixed library-owned device region (16 MiB per device); such
+ * calls on one device are ordered by an event, calls that do not split share nothing.
+ * UNDER STREAM CAPTURE a call never splits, so a captured replay of a shape that
+ * splits eagerly gives a result that differs from the eager one by rounding (the
+ * merge stores fp16 partials); both meet the BF16 tolerance. */
 int mx_flash_attn(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
                   void* stream);
 
@@ -83,10 +90,10 @@ int mx_flash_attn_uses_mfma(const void* q, const void* k, const void* v, const v
  * work of these parameters on a device with `cus` compute units (cus <= 0: the current
  * device). The first *full units (head, 256-query tile) run whole; each of the last
  * *units units runs as *parts key ranges whose partial outputs a merge kernel combines
- * (parts == 1: no split). A split call keeps its partials in a library-held device
- * region (allocated on first use, grown on demand, one per device, calls ordered by an
- * event); under stream capture, for causal calls and when that region cannot be
- * allocated the call runs unsplit. Launches nothing. */
+ * (parts == 1: no split). A split call keeps its partials in a fixed 16 MiB device
+ * region (one per device, calls ordered by an event); only splits whose partials fit it
+ * are planned. Causal calls and calls under stream capture run unsplit. Launches
+ * nothing. */
 int mx_flash_attn_split_plan(const mx_attn_params* p, int cus, int* full, int* units, int* parts);
 
 /* No counterpart in the reference. For callers that cannot allocate device memory
@@ -95,9 +102,12 @@ int mx_flash_attn_split_plan(const mx_attn_params* p, int cus, int* full, int* u
  * of 128 MiB (one per device, held until the process ends) instead of an argument.
  * Allocates nothing. Shapes whose workspace (mx_flash_attn_fp8_workspace) exceeds the
  * scratch return MX_E_UNSUPPORTED; arguments the quantized path does not take fall
- * back to mx_flash_attn, as in mx_flash_attn_fp8. Every call on a device shares that
- * device's scratch: calls that overlap on one device (other streams, other host
- * threads) race and must be serialised by the caller. */
+ * back to mx_flash_attn, as in mx_flash_attn_fp8 (which allocates nothing either).
+ * Every call on a device shares that device's scratch; eager calls are ordered by a
+ * per-device event (a call on another stream or host thread waits on the device for
+ * the previous call to finish). Calls under stream capture skip that event: a graph
+ * replay that overlaps another call on the same device races on the scratch, and the
+ * caller must serialise them. */
 int mx_flash_attn_fp8_noalloc(const void* q, const void* k, const void* v, void* o, const mx_attn_params* p,
                               void* stream);
 

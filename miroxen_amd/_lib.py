@@ -9,9 +9,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-# MIROXEN_ATTN_LIB may point at another build of the same library (A/B timing of
-# kernel variants); by default the in-tree build is loaded.
-LIB_PATH = os.environ.get("MIROXEN_ATTN_LIB") or os.path.join(HERE, "lib", "libmiroxen_attn.so")
+LIB_PATH = os.path.join(HERE, "lib", "libmiroxen_attn.so")
 
 MX_OK, MX_E_INVALID, MX_E_HIP, MX_E_UNSUPPORTED = 0, -1, -2, -3
 

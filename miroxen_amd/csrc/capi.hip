@@ -134,27 +134,39 @@ bool fast_bf16_ok(const void* q, const void* k, const void* v, const void* o, co
 // caller allocation. Host code never passes the array's name to a kernel or a copy:
 // on the host it is a stand-in symbol, and each device's copy is at its own address,
 // looked up once per device with hipGetSymbolAddress (with that device current).
+// Calls on one device are ordered through a per-device event (each call's stream
+// waits for the previous call's last kernel), so calls on different streams do not
+// overwrite each other's workspace; calls under stream capture skip the event (a
+// graph cannot wait on work outside it), so a replay that overlaps another call on
+// the device races on the scratch.
 constexpr size_t kNoAllocScratchBytes = size_t(128) << 20;  // 128 MiB
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices];
+struct ScratchDevice {
+  std::once_flag once;
+  hipError_t setup = hipSuccess;
+  void* ptr = nullptr;
+  hipEvent_t done = nullptr;
+  std::mutex mu;
+};
+ScratchDevice g_scratch[kMaxDevices];
 
-int scratch_of_current_device(void** out) {
+int scratch_of_current_device(ScratchDevice** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_status(e, "flash_attn_fp8_noalloc");
   if (dev < 0 || dev >= kMaxDevices) return fail(MX_E_UNSUPPORTED, "flash_attn_fp8_noalloc: device %d", dev);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
+  ScratchDevice& S = g_scratch[dev];
+  std::call_once(S.once, [&S] {
     void* ptr = nullptr;
-    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess) return hip_status(e, "flash_attn_fp8_noalloc: scratch address");
-    if (!ptr || !aligned(ptr, 256))
-      return fail(MX_E_HIP, "flash_attn_fp8_noalloc: scratch address not 256-byte aligned");
-    g_scratch_ptr[dev] = ptr;
-  }
-  *out = g_scratch_ptr[dev];
+    hipError_t r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (r == hipSuccess && (!ptr || !aligned(ptr, 256))) r = hipErrorInvalidValue;
+    if (r == hipSuccess) r = hipEventCreateWithFlags(&S.done, hipEventDisableTiming);
+    if (r == hipSuccess) S.ptr = ptr;
+    S.setup = r;
+  });
+  if (S.setup != hipSuccess) return hip_status(S.setup, "flash_attn_fp8_noalloc: scratch set-up");
+  *out = &S;
   return MX_OK;
 }
 
@@ -282,15 +294,27 @@ int mx_flash_attn_fp8_noalloc(const void* q, const void* k, const void* v, void*
   if (need > kNoAllocScratchBytes)
     return fail(MX_E_UNSUPPORTED, "flash_attn_fp8_noalloc: workspace of %zu bytes exceeds the %zu-byte scratch",
                 need, kNoAllocScratchBytes);
-  void* ws = nullptr;
-  rc = scratch_of_current_device(&ws);
+  ScratchDevice* S = nullptr;
+  rc = scratch_of_current_device(&S);
   if (rc) return rc;
+  auto st = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(st, &cap);
+  if (e != hipSuccess) return hip_status(e, "flash_attn_fp8_noalloc");
+  const bool ordered = cap == hipStreamCaptureStatusNone;
+  std::unique_lock<std::mutex> lock(S->mu, std::defer_lock);
+  if (ordered) {
+    lock.lock();
+    e = hipStreamWaitEvent(st, S->done, 0);
+    if (e != hipSuccess) return hip_status(e, "flash_attn_fp8_noalloc");
+  }
   // the prologue rewrites every region the attention kernel reads and zeroes the
   // split arrival counters, so nothing is left over from the previous call
-  return hip_status(mxa::launch_sage_fp8(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                                         static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), a,
-                                         static_cast<char*>(ws), static_cast<hipStream_t>(stream)),
-                    "flash_attn_fp8_noalloc");
+  e = mxa::launch_sage_fp8(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                           static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), a,
+                           static_cast<char*>(S->ptr), st);
+  if (e == hipSuccess && ordered) e = hipEventRecord(S->done, st);
+  return hip_status(e, "flash_attn_fp8_noalloc");
 }
 
 int mx_sage_quantize(const void* q, const void* k, const void* v, const mx_attn_params* p, void* ws,

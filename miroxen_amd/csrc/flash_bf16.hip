@@ -27,6 +27,7 @@
 //    than all waves in lockstep. Within an MFMA phase, sched_group_barrier keeps
 //    LDS operand reads a few MFMAs ahead of use (kKPrefetch / kVPrefetch).
 //  * Work-groups are remapped so one head's query tiles share an XCD (and its L2).
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 #include <utility>
@@ -558,6 +559,25 @@ bf16_split_merge(uint16_t* __restrict__ o, mx_attn_params p, BfSplit sp) {
 
 namespace {
 
+struct Bf16Plan {
+  int full, units, parts;
+};
+constexpr int kBfMaxParts = 8;
+
+// Split partials: ml [units][parts][256] {m, l, scale, 0} f32, then po
+// [units][parts][256][D] fp16.
+size_t bf16_split_bytes(int units, int parts, int D) {
+  const size_t blocks = size_t(units) * parts * 256;
+  return blocks * sizeof(f32x4) + (blocks * D * 2 + 255) / 256 * 256;
+}
+
+// The split partials live in this fixed region, one copy per device, held until the
+// process ends: the library never allocates on the launch path. 16 MiB holds, at
+// D = 128, 240 parts of 256 queries (e.g. 30 units x 8 parts, 48 x 5); the plan only
+// considers splits that fit.
+constexpr size_t kBfSplitBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char bf16_split_scratch[kBfSplitBytes];
+
 // Split plan for a non-causal grid of U units on C CUs (one work-group per CU). The
 // chip is power-limited: a CU runs a 64-key tile in ~1.29 us (D = 128) while at most
 // ~165 CUs are busy, and the clock drops as more are (~2.0 us per tile with all 256
@@ -568,12 +588,8 @@ namespace {
 // each part nt/S tiles plus ~2 tiles of fixed work (Q load, first tiles, partial
 // store), then the merge (partial bytes at ~3 TB/s plus ~4 us) and ~3 us for the
 // second launch when whole rounds precede it. S minimises the estimate; no split
-// unless it wins by 5 %. Measured: U = 2..32 units 1.9-3.2x faster, config-2 shape
+// unless it wins by 5 %, and only splits whose partials fit the fixed region. Measured: U = 2..32 units 1.9-3.2x faster, config-2 shape
 // (408 units, r = 152) and 120 units of 17 tiles unsplit.
-struct Bf16Plan {
-  int full, units, parts;
-};
-constexpr int kBfMaxParts = 8;
 Bf16Plan bf16_plan(const mx_attn_params& p, int C) {
   constexpr int QT = 256;
   const int64_t U64 = int64_t((p.Sq + QT - 1) / QT) * p.Hq;
@@ -588,6 +604,7 @@ Bf16Plan bf16_plan(const mx_attn_params& p, int C) {
   const double whole = nt * tile_s(r);
   double best = 0.95 * whole;
   for (int S = 2; S <= kBfMaxParts && S * 4 <= nt; ++S) {
+    if (bf16_split_bytes(r, S, p.D) > kBfSplitBytes) break;
     double cost = U > r ? 3e-6 : 0.0;
     for (int64_t left = int64_t(r) * S; left > 0; left -= C)
       cost += (double(nt) / S + 2.0) * tile_s(int(left < C ? left : C));
@@ -597,25 +614,43 @@ Bf16Plan bf16_plan(const mx_attn_params& p, int C) {
   if (pl.parts > 1) pl.full = U - r, pl.units = r;
   return pl;
 }
-size_t bf16_split_bytes(const Bf16Plan& pl, int D) {
-  const size_t blocks = size_t(pl.units) * pl.parts * 256;
-  return blocks * sizeof(f32x4) + (blocks * D * 2 + 255) / 256 * 256;
+
+// Per-device state of the split. cus is read without a lock (every thread that races
+// to fill it stores the same value). The region's address and the ordering event are
+// set up once per device, on the first call that splits; after that a split call
+// takes the device's mutex only to order itself after the previous split call
+// (stream wait on the event, launches, event record), so calls on different streams
+// never share the region at the same time. Calls that do not split (the large grids,
+// causal calls, calls under stream capture) take no lock and touch no shared state.
+constexpr int kMaxDev = 64;
+struct SplitDevice {
+  std::atomic<int> cus{0};
+  std::once_flag once;
+  hipError_t setup = hipSuccess;
+  void* region = nullptr;
+  hipEvent_t done = nullptr;
+  std::mutex mu;
+};
+SplitDevice g_split[kMaxDev];
+
+int device_cus(SplitDevice& R, int dev) {
+  int n = R.cus.load(std::memory_order_relaxed);
+  if (n == 0 && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+    R.cus.store(n, std::memory_order_relaxed);
+  return n;
 }
 
-// Library-held region for the split partials, one per device, grown on demand. Calls
-// that use it are ordered by a per-device event (a call on another stream waits for
-// the previous split's merge), so concurrent calls never share it. The split is not
-// used under stream capture or when the region cannot be allocated: the call then runs
-// as one launch.
-constexpr int kMaxDev = 64;
-struct SplitRegion {
-  std::mutex mu;
-  void* buf = nullptr;
-  size_t bytes = 0;
-  hipEvent_t done = nullptr;
-  int cus = 0;
-};
-SplitRegion g_split[kMaxDev];
+hipError_t split_setup(SplitDevice& R) {
+  std::call_once(R.once, [&R] {
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(bf16_split_scratch));
+    if (e == hipSuccess && (!ptr || reinterpret_cast<uintptr_t>(ptr) % 256)) e = hipErrorInvalidValue;
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&R.done, hipEventDisableTiming);
+    if (e == hipSuccess) R.region = ptr;
+    R.setup = e;
+  });
+  return R.setup;
+}
 
 }  // namespace
 
@@ -626,7 +661,7 @@ int flash_bf16_split_plan(const mx_attn_params& p, int cus, int* full, int* unit
 }
 
 // Launch the fast path. Preconditions (checked by the caller): D in {64, 72, 128},
-// q/k/v/o 2-byte aligned, Skv * kv_stride * 2 < 2^32.
+// q/k/v/o 2-byte aligned, Skv * kv_stride * 2 < 2^32. No allocation, no host sync.
 hipError_t launch_flash_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                              const mx_attn_params& p, hipStream_t s) {
   const float c = __builtin_fabsf(p.scale) * kLog2e;
@@ -638,36 +673,21 @@ hipError_t launch_flash_bf16(const uint16_t* q, const uint16_t* k, const uint16_
   if (p.D != 128 && p.D != 64 && p.D != 72) return hipErrorInvalidValue;
   const bool cz = p.causal != 0;
 
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  SplitRegion* R = dev >= 0 && dev < kMaxDev ? &g_split[dev] : nullptr;
-  std::unique_lock<std::mutex> lock;
   Bf16Plan pl{int(blocks), 0, 1};
-  if (R && !cz) {
-    lock = std::unique_lock<std::mutex>(R->mu);
-    if (!R->cus) {
-      int n = 0;
-      if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) R->cus = n;
+  SplitDevice* R = nullptr;
+  if (!cz) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev >= 0 && dev < kMaxDev) {
+      R = &g_split[dev];
+      pl = bf16_plan(p, device_cus(*R, dev));
     }
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
-    if (cap == hipStreamCaptureStatusNone) pl = bf16_plan(p, R->cus);
     if (pl.parts > 1) {
-      const size_t need = bf16_split_bytes(pl, p.D);
-      if (R->bytes < need) {
-        if (R->buf) {  // the previous region may still be read by an earlier merge
-          if (R->done && hipEventSynchronize(R->done) != hipSuccess) pl = Bf16Plan{int(blocks), 0, 1};
-          else if (hipFree(R->buf) == hipSuccess) R->buf = nullptr, R->bytes = 0;
-        }
-        if (pl.parts > 1 && !R->buf) {
-          void* b = nullptr;
-          if (hipMalloc(&b, need) == hipSuccess) R->buf = b, R->bytes = need;
-          else (void)hipGetLastError();
-        }
-        if (R->bytes < need) pl = Bf16Plan{int(blocks), 0, 1};
-      }
-      if (pl.parts > 1 && !R->done && hipEventCreateWithFlags(&R->done, hipEventDisableTiming) != hipSuccess)
+      // a captured graph may replay while eager calls use the region: capture runs unsplit
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone ||
+          split_setup(*R) != hipSuccess)
         pl = Bf16Plan{int(blocks), 0, 1};
     }
   }
@@ -684,11 +704,12 @@ hipError_t launch_flash_bf16(const uint16_t* q, const uint16_t* k, const uint16_
     }
     run(flash_bf16_pp<DH, false, false>, pl.full);
     if (pl.parts > 1) {
+      std::lock_guard<std::mutex> lock(R->mu);
       hipError_t e2 = hipStreamWaitEvent(s, R->done, 0);
       if (e2 != hipSuccess) return e2;
       const size_t blocks_ml = size_t(pl.units) * pl.parts * 256;
-      sp.ml = static_cast<f32x4*>(R->buf);
-      sp.po = reinterpret_cast<uint16_t*>(static_cast<char*>(R->buf) + blocks_ml * sizeof(f32x4));
+      sp.ml = static_cast<f32x4*>(R->region);
+      sp.po = reinterpret_cast<uint16_t*>(static_cast<char*>(R->region) + blocks_ml * sizeof(f32x4));
       run(flash_bf16_pp<DH, false, true>, int64_t(pl.units) * pl.parts);
       const int64_t threads = int64_t(pl.units) * QT * (DH / 8);
       hipLaunchKernelGGL(bf16_split_merge<DH>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, o, p, sp);

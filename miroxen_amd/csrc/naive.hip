@@ -3,9 +3,8 @@
 // (src/kernels/attention.cu:292-348): fp32 dot products, expf, online
 // max/sum over 128-key chunks, bf16 output, 0 when the row has no live key.
 // Extended with the key-padding mask. Besides attn_reference it is the general
-// path of flash_attn where the MFMA kernel's preconditions fail (token strides not a
-// multiple of 8 elements or operands not 16-byte aligned, masked Skv > 65536, K/V
-// beyond 32-bit buffer offsets).
+// path of flash_attn where the MFMA kernel's preconditions fail (operands not 2-byte
+// aligned, masked Skv > 65536, K/V beyond 32-bit buffer offsets).
 #include "attn_common.hpp"
 
 namespace mxa {

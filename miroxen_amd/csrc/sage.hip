@@ -1133,8 +1133,9 @@ mx_sage_layout sage_layout(const mx_attn_params& p) {
   return L;
 }
 
-// Prologue: preconditions checked by the caller (D == 64 or 128, q/k/v 16-byte aligned,
-// strides % 8 == 0, ws 256-byte aligned and large enough).
+// Prologue: preconditions checked by the caller (fp8_ok: D == 64 or 128, q/k/v 2-byte
+// aligned with any token stride, skv_pad * D < 2^32 for the 32-bit buffer offsets; ws
+// 256-byte aligned and large enough).
 // nr: null for the plain prologue, else {Q norm/rope, K norm/rope} applied on the fly
 // (D == 128 and nr128_supported, checked by the caller).
 template <int D>

@@ -31,6 +31,26 @@ def test_library_exports_every_declared_symbol():
     assert "gfx950" in L.mx_version().decode()
 
 
+def test_library_imports_no_allocation_or_sync_api():
+    """The reference's entry points do pure launches (attention.cu:411-458): no
+    allocation, no host synchronisation. The library holds its split partials and the
+    no-alloc scratch in fixed device arrays, so its dynamic imports contain no
+    allocating, freeing or synchronising HIP call at all."""
+    import shutil
+    import subprocess
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--undefined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    imported = {line.split()[-1].split("@")[0] for line in out.splitlines() if line.strip()}
+    hip = sorted(n for n in imported if n.startswith("hip"))
+    assert "hipLaunchKernel" in hip
+    bad = [n for n in hip if re.search(r"Malloc|Free|Alloc|Synchronize|hipMemcpy(?!.*Async)|hipMemset(?!.*Async)",
+                                       n)]
+    assert not bad, bad
+
+
 def test_struct_layout_matches_header():
     # int x5, float, int x2, int64 x3, pointer: 8 4-byte fields = 32 bytes, then 3*8 + 8
     assert ctypes.sizeof(_lib.CParams) == 32 + 24 + 8

@@ -268,6 +268,19 @@ def test_fallbacks_and_aliasing(cuda):
     flash_attn_fp8(qa, k, v, qa, p, ws)
     torch.cuda.synchronize()
     assert torch.equal(qa.view(torch.int16), sep.view(torch.int16))
+    # o aliasing q on a layout whose grid is split (config 3's shape): the split
+    # parts and the last-arrival merge still read every Q row before any output row
+    # of the unit is written
+    cfg = CONFIGS[3]
+    q3, k3, v3, m3 = make_inputs(cfg, seed=19, device=cuda)
+    p3 = AttnParams(Sq=cfg.S, Skv=cfg.S, Hq=cfg.H, Hkv=cfg.H, D=128, kv_valid=m3)
+    assert sage_layout(p3)["split_parts"] > 1
+    ws3 = _ws(p3, cuda)
+    sep3 = torch.empty_like(q3)
+    flash_attn_fp8(q3, k3, v3, sep3, p3, ws3)
+    flash_attn_fp8(q3, k3, v3, q3, p3, ws3)
+    torch.cuda.synchronize()
+    assert torch.equal(q3.view(torch.int16), sep3.view(torch.int16))
     # misaligned workspace is rejected
     with pytest.raises(RuntimeError, match="256-byte aligned"):
         flash_attn_fp8(q, k, v, o, p, ws.data_ptr() + 16)
