@@ -50,6 +50,97 @@ def _time(fn, steps: int, warmup: int, warm_s: float) -> float:
     return e0.elapsed_time(e1) / steps
 
 
+MAX_GFX_MHZ = 2400.0  # MI355X maximum shader clock (the nominal peaks assume it)
+
+
+class _Smi:
+    """Board telemetry through amdsmi (the library behind amd-smi): per-XCD shader clock,
+    the socket energy accumulator (15.3 uJ units) and the power-limit (PPT) residency
+    counter. Absent or failing telemetry yields None; it never affects the timing."""
+
+    def __init__(self):
+        self.h = None
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            self.smi = amdsmi
+            self.h = amdsmi.amdsmi_get_processor_handles()[0]
+            self.res = float(amdsmi.amdsmi_get_energy_count(self.h)["counter_resolution"])
+        except Exception:
+            self.h = None
+            return
+        self.board = {}
+        try:
+            self.board["power_limit_w"] = amdsmi.amdsmi_get_power_info(self.h)["power_limit"] / 1e6
+            self.board["max_gfx_mhz"] = amdsmi.amdsmi_get_clock_info(self.h, amdsmi.AmdSmiClkType.GFX)["max_clk"]
+        except Exception:
+            pass
+
+    def metrics(self):
+        if self.h is None:
+            return None
+        try:
+            return self.smi.amdsmi_get_gpu_metrics_info(self.h)
+        except Exception:
+            return None
+
+
+_SMI = None
+
+
+def _telemetry(fn, batch: int = 32, max_seconds: float = 3.0):
+    """Shader clock and board power of one leg, from back-to-back calls of the leg's own
+    call right after its timed region. The firmware refreshes the metrics table about
+    once a second, so the window runs from the first refresh seen under load to the
+    next one: power = energy-accumulator delta over the table's own timestamp delta
+    (ns), clock = the per-XCD shader clocks of those refreshes (mean over XCDs and
+    refreshes), ppt_residency = share of the window the firmware counted at the power
+    limit."""
+    import torch
+    global _SMI
+    if _SMI is None:
+        _SMI = _Smi()
+    first = _SMI.metrics()
+    if first is None:
+        return None
+    snaps = []
+    last_ts = first.get("system_clock_counter")
+    t0 = time.perf_counter()
+    while len(snaps) < 2 and time.perf_counter() - t0 < max_seconds:
+        for _ in range(batch):
+            fn()
+        torch.cuda.synchronize()
+        m = _SMI.metrics()
+        if m is not None and m.get("system_clock_counter") != last_ts:
+            last_ts = m.get("system_clock_counter")
+            snaps.append(m)
+    if len(snaps) < 2:
+        return None
+    a, b = snaps
+    out = {}
+    try:
+        clocks = [x for m in snaps for x in m["current_gfxclks"] if isinstance(x, (int, float)) and x > 0]
+        if clocks:
+            out["gfx_mhz"] = round(sum(clocks) / len(clocks), 1)
+        dts = (b["system_clock_counter"] - a["system_clock_counter"]) * 1e-9
+        out["window_s"] = round(dts, 3)
+        out["socket_w"] = round((b["energy_accumulator"] - a["energy_accumulator"]) * _SMI.res * 1e-6 / dts, 1)
+        dacc = b["accumulation_counter"] - a["accumulation_counter"]
+        if dacc > 0:
+            out["ppt_residency"] = round((b["ppt_residency_acc"] - a["ppt_residency_acc"]) / dacc, 3)
+    except (KeyError, TypeError, ZeroDivisionError):
+        pass
+    return out
+
+
+def _at_clock(achieved: float, peak: float, tel) -> dict:
+    """Roofline fraction against the peak scaled to the measured shader clock."""
+    if not tel or "gfx_mhz" not in tel:
+        return {}
+    p = peak * tel["gfx_mhz"] / MAX_GFX_MHZ
+    return {"peak_at_clock": round(p, 1), "frac_at_clock": round(achieved / p, 4)}
+
+
 def _traffic(name: str):
     """HBM bytes per launch measured with rocprofv3 --pmc (committed summary), or None."""
     path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
@@ -90,6 +181,60 @@ def cpu_baseline(q, k, v, mask, S, H, D, budget_s: float = 12.0):
             "host_cpus": os.cpu_count(), "cpu_model": model,
             "sample": f"{n} of {S} query rows x {H} heads, all {S} keys, {dt:.1f} s; "
                       f"full call extrapolated {dt * S / n * 1e3:.0f} ms"}
+
+
+def cpu_baseline_config1() -> dict:
+    """The CPU oracle on config 1 (the reference's CPU-runnable case: H=24, S=1088, D=128,
+    no mask) as a full call, every query row."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from miroxen_amd.synth import CONFIGS, attn_flops, make_inputs
+    c = CONFIGS[1]
+    threads = min(os.cpu_count() or 1, 16)
+    q, k, v, _ = make_inputs(c, seed=1)
+    bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    t0 = time.perf_counter()
+    oracle.attention_f64(bits(q), bits(k), bits(v), c.S, c.S, c.H, c.H, c.D, threads=threads)
+    dt = time.perf_counter() - t0
+    return {"value": round(attn_flops(c.H, c.S, c.S, c.D) / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port", "ms": round(dt * 1e3, 1),
+            "sample": f"config 1 full call ({c.S} rows x {c.H} heads x {c.S} keys), {dt:.2f} s"}
+
+
+def cpu_baseline_sage(q, k, v, mask, S, H, D, budget_s: float = 8.0) -> dict:
+    """The Sage path on the CPU: the oracle's prologue (K mean, V abs-max, INT8 Q/K, e4m3
+    V^T) over the whole config-3 input, then its emulator of the quantized kernel (exact
+    int32 scores, e4m3 P, fp32 accumulation; OpenMP over (row, head)) on a bounded sample
+    of query rows; the full call is the prologue plus the emulator extrapolated."""
+    import numpy as np
+    import torch
+
+    import oracle
+    threads = min(os.cpu_count() or 1, 16)
+    bits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    qb, kb, vb = bits(q), bits(k), bits(v)
+    mk = None if mask is None else mask.cpu().numpy()
+    t0 = time.perf_counter()
+    _, t = oracle.sage_reference(qb, kb, vb, S, S, H, H, D, kv_valid=mk, rows=np.zeros(0, np.int32),
+                                 threads=threads)
+    t_pro = time.perf_counter() - t0
+    args = (t["qi"], t["ki"], t["vt"], t["qs"], t["ks"], t["va"], S, S, H, H, D)
+    probe = np.arange(0, S, max(1, S // 16), dtype=np.int32)[:16]
+    t0 = time.perf_counter()
+    oracle.sage_emulate(*args, kv_valid=mk, rows=probe, threads=threads)
+    dt = max(time.perf_counter() - t0, 1e-3)
+    n = int(min(S, max(16, len(probe) * budget_s / dt)))
+    rows = np.linspace(0, S - 1, n).astype(np.int32)
+    t0 = time.perf_counter()
+    oracle.sage_emulate(*args, kv_valid=mk, rows=rows, threads=threads)
+    dt = time.perf_counter() - t0
+    full = t_pro + dt * S / n
+    flop = 4.0 * H * S * S * D
+    return {"value": round(flop / full / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"prologue over all {S} tokens {t_pro:.2f} s + emulator on {n} of {S} query rows x {H} "
+                      f"heads, {dt:.1f} s; full call extrapolated {full * 1e3:.0f} ms"}
 
 
 BS_M, BS_N, BS_K = 8192, 12288, 4096  # the reference's quoted block-scaled GEMM shape (src/kernels/blockscale.h:2)
@@ -270,6 +415,7 @@ def main() -> int:
     ms = _time(lambda: flash_attn(q, k, v, o, p), args.steps, args.warmup, args.warm_seconds)
     wall = time.perf_counter() - t0
     tflops = flop / (ms * 1e-3) / 1e12
+    tel_bf16 = _telemetry(lambda: flash_attn(q, k, v, o, p))
 
     # ---- Sage INT8/FP8 on config 3 ----
     c3 = CONFIGS[3]
@@ -279,7 +425,9 @@ def main() -> int:
     o3 = torch.empty_like(q3)
     ms_e2e = _time(lambda: flash_attn_fp8(q3, k3, v3, o3, p3, ws), args.steps, args.warmup, args.warm_seconds)
     ms_pro = _time(lambda: sage_quantize(q3, k3, v3, p3, ws), args.steps, args.warmup, args.warm_seconds)
+    tel_e2e = _telemetry(lambda: flash_attn_fp8(q3, k3, v3, o3, p3, ws))
     ms_main = _time(lambda: sage_attend(o3, p3, ws), args.steps, args.warmup, args.warm_seconds)
+    tel_main = _telemetry(lambda: sage_attend(o3, p3, ws))
     # config 3's stated Q grouping (one scale per 64-token block) beside the reference's 16
     ms_pro64 = _time(lambda: sage_quantize(q3, k3, v3, p3, ws, q_group=64), args.steps, args.warmup,
                      args.warm_seconds)
@@ -304,7 +452,9 @@ def main() -> int:
                       "tflops_end_to_end": round(flop / (ms_e2e64 * 1e-3) / 1e12, 2)},
         "roofline": {"bound": "mfma", "achieved": round(flop / (ms_main * 1e-3) / 1e12, 2), "peak": PEAK_FP8,
                      "unit": "TFLOP/s", "frac": round(flop / (ms_main * 1e-3) / 1e12 / PEAK_FP8, 4),
-                     "traffic": _traffic("sage_attn_config3")},
+                     "traffic": _traffic("sage_attn_config3"),
+                     **_at_clock(flop / (ms_main * 1e-3) / 1e12, PEAK_FP8, tel_main)},
+        "telemetry_end_to_end": tel_e2e, "telemetry_kernel": tel_main,
     }
 
     # ---- head_norm_rope fused into the Sage prologue (config-3 shape, Qwen-Image-style
@@ -348,6 +498,19 @@ def main() -> int:
 
     # ---- the other BASELINE configs at their full shapes (BF16 and Sage each) ----
     others = {}
+    c1 = CONFIGS[1]
+    q1, k1, v1, _ = make_inputs(c1, seed=1, device=dev)
+    p1 = AttnParams(Sq=c1.S, Skv=c1.S, Hq=c1.H, Hkv=c1.H, D=c1.D)
+    o1 = torch.empty_like(q1)
+    w1 = torch.empty(flash_attn_fp8_workspace(p1), dtype=torch.uint8, device=dev)
+    f1 = attn_flops(c1.H, c1.S, c1.S, c1.D)
+    m1 = _time(lambda: flash_attn(q1, k1, v1, o1, p1), args.steps, args.warmup, args.warm_seconds)
+    m1e = _time(lambda: flash_attn_fp8(q1, k1, v1, o1, p1, w1), args.steps, args.warmup, args.warm_seconds)
+    others["config1"] = {"workload": c1.name, "H": c1.H, "S": c1.S, "steps": args.steps,
+                         "bf16_ms": round(m1, 4), "bf16_tflops": round(f1 / (m1 * 1e-3) / 1e12, 1),
+                         "sage_ms_end_to_end": round(m1e, 4),
+                         "sage_tflops_end_to_end": round(f1 / (m1e * 1e-3) / 1e12, 1)}
+    del q1, k1, v1, o1, w1
     if not args.skip_large:
         del q3, k3, v3, o3, ws, t, qd, kd, vd, wsn
         for cid in (4, 5):
@@ -364,11 +527,14 @@ def main() -> int:
             # attention kernel quantizes Q itself) does not write
             sage_quantize(qc, kc, vc, pc, wc)
             mk = _time(lambda: sage_attend(oc, pc, wc), n, args.warmup, args.warm_seconds)
+            tb = _telemetry(lambda: flash_attn(qc, kc, vc, oc, pc), batch=4)
+            ts = _telemetry(lambda: sage_attend(oc, pc, wc), batch=4)
             others[f"config{cid}"] = {
                 "workload": c.name, "H": c.H, "S": c.S, "steps": n,
                 "bf16_ms": round(mb, 3), "bf16_tflops": round(fc / (mb * 1e-3) / 1e12, 1),
                 "sage_ms_end_to_end": round(me, 3), "sage_tflops_end_to_end": round(fc / (me * 1e-3) / 1e12, 1),
-                "sage_tflops_kernel": round(fc / (mk * 1e-3) / 1e12, 1)}
+                "sage_tflops_kernel": round(fc / (mk * 1e-3) / 1e12, 1),
+                "telemetry_bf16": tb, "telemetry_sage_kernel": ts}
             del qc, kc, vc, oc, wc
 
     # ---- BF16 beyond the BASELINE configs: causal at config 2's shape (useful FLOP =
@@ -412,7 +578,10 @@ def main() -> int:
                    "kernel": version()},
         "frac_bf16_peak": round(tflops / PEAK_BF16, 4),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_BF16, 4), "traffic": traffic},
+                     "frac": round(tflops / PEAK_BF16, 4), "traffic": traffic,
+                     **_at_clock(tflops, PEAK_BF16, tel_bf16)},
+        "telemetry": tel_bf16,
+        "board": getattr(_SMI, "board", None),
         "sage": sage,
         "other_configs": others,
         "extras": extras,
@@ -421,6 +590,9 @@ def main() -> int:
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(q, k, v, mask, S, H, D)
+        line["cpu_baseline_config1"] = cpu_baseline_config1()
+        q3, k3, v3, m3 = make_inputs(c3, seed=3, device=dev)
+        line["sage"]["cpu_baseline"] = cpu_baseline_sage(q3, k3, v3, m3, S, H, D)
     print(json.dumps(line), flush=True)
     return 0
 
