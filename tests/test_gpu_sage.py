@@ -199,8 +199,11 @@ def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
     c_emu, e_emu = cosine(got, emu), max_abs(got, emu)
     c_ex, rr = cosine(got, exact), rel_rms(got, exact)
     rr_ref = rel_rms(ref_rule, exact)
+    h2 = oracle.sage_emulate(g["qi"], g["ki"], g["vt"], g["qs"], g["ks"], g["va"], S, S, H, H, 128,
+                             kv_valid=mk, rows=rows, headroom=2.0)
     print(f"{seed_note} sage: cos(emu)={c_emu:.7f} maxabs(emu)={e_emu:.3g} cos(exact)={c_ex:.6f} relrms={rr:.4f} "
-          f"relrms(reference rule)={rr_ref:.4f}", flush=True)
+          f"relrms(emulator H=0 reference rule / H=2 / H=3 kernel rule)={rr_ref:.4f} / {rel_rms(h2, exact):.4f} / "
+          f"{rel_rms(emu, exact):.4f}", flush=True)
     # emulator fed the same workspace: accumulation order and the bf16 store differ, and
     # the GPU's exp2 (v_exp_f32, within 1 ulp) against libm's can move a probability across
     # an e4m3 rounding boundary, one e4m3 step (2^-4 relative) of that key's weight
@@ -208,9 +211,10 @@ def _sage_vs_oracle(cuda, q, k, v, mask, S, H, rows, seed_note=""):
     # Cosine >= 0.995 against exact attention, and the reference's 4 % rel-RMS gate
     # (tests/attention_fp8_test.cpp:65) unless the reference's own arithmetic (exact-max
     # emulator on the same quantized operands) already exceeds it on this input: then
-    # the kernel is held to that figure plus 0.25 points.
+    # the kernel is held to that figure plus 0.1 points (the lazy max's 2^-3 scaling of P
+    # gives up three binades of e4m3's normal range at the small-weight end).
     assert c_ex >= 0.995
-    assert rr < max(0.04, rr_ref + 0.0025), (rr, rr_ref)
+    assert rr < max(0.04, rr_ref + 0.001), (rr, rr_ref)
     return o
 
 
