@@ -147,6 +147,51 @@ __device__ __forceinline__ void build_live(uint64_t* live, const mx_attn_params&
     }
   }
 }
+// The same bitmaps from 16-byte loads when the mask is 16-byte aligned: lane i of a
+// wave loads keys 16i..16i+15 of a 1024-key chunk (16 tiles) through a buffer
+// resource ending at Skv (keys past it read as 0: dead), folds each byte to one bit
+// and stores the 16 bits as entry 64c + i of the table viewed as uint16, so the
+// table's uint64 t holds tile t's 64 keys in order. Wave w loads chunks w and w + NW
+// first (live16_issue, before the caller's other loads, so their latencies overlap)
+// and folds them, then any further chunks (live16_finish).
+struct Live16 {
+  u32x4 w[2];
+};
+__device__ __forceinline__ u32x4 live16_load(const mx_attn_params& p, int c, int lane) {
+  const __amdgpu_buffer_rsrc_t r = buf_rsrc(p.kv_valid, uint32_t(p.Skv));
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, uint32_t(c * 1024 + lane * 16), 0, 0));
+}
+__device__ __forceinline__ void live16_store(uint64_t* live, u32x4 w, int c, int lane) {
+  uint32_t bits = 0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t x = w[d];
+    const uint32_t hi = ((x & 0x7f7f7f7fu) + 0x7f7f7f7fu) | x;  // byte's top bit set iff the byte is nonzero
+    bits |= ((((hi >> 7) & 0x01010101u) * 0x01020408u) >> 24) << (4 * d);
+  }
+  if (c * 16 + (lane >> 2) < kMaxLiveTiles) reinterpret_cast<uint16_t*>(live)[c * 64 + lane] = uint16_t(bits);
+}
+template <int NW>
+__device__ __forceinline__ Live16 live16_issue(const mx_attn_params& p, int nt, int wave, int lane) {
+  const int nch = (nt + 15) / 16;
+  Live16 L;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = wave + j * NW;
+    L.w[j] = c < nch ? live16_load(p, c, lane) : u32x4{0, 0, 0, 0};
+  }
+  return L;
+}
+template <int NW>
+__device__ __forceinline__ void live16_finish(uint64_t* live, const Live16& L, const mx_attn_params& p, int nt,
+                                              int wave, int lane) {
+  const int nch = (nt + 15) / 16;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (wave + j * NW < nch) live16_store(live, L.w[j], wave + j * NW, lane);
+  for (int c = wave + 2 * NW; c < nch; c += NW) live16_store(live, live16_load(p, c, lane), c, lane);
+}
+
 template <int KT>
 __device__ __forceinline__ uint64_t tile_live(const uint64_t* live, const mx_attn_params& p, int t) {
   if (p.kv_valid) return live[t];

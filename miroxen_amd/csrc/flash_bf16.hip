@@ -330,6 +330,38 @@ __device__ __forceinline__ void store_block(const QBlock<DH>& X, uint16_t* o, co
     }
 }
 
+// The same store through LDS (D = 64 / 128, o 16-byte aligned, o_stride % 8 == 0): the
+// wave writes its 32 x DH output block into its own LDS region (16-byte chunks of row
+// n XOR-swizzled by n), then every lane stores 16 contiguous bytes, so one store
+// instruction writes 1 KB of whole rows instead of 4-byte pieces of 32 rows. The
+// caller has passed a work-group barrier after the tile loop (the region is a K/V
+// buffer).
+template <int DH>
+__device__ __forceinline__ void store_block_lds(const QBlock<DH>& X, uint16_t* o, const mx_attn_params& p,
+                                                int row0, int head, const Lane& ln, unsigned char* wbuf) {
+  static_assert(DH % 32 == 0, "whole 16-byte chunks per wave half");
+  constexpr int CH = DH / 8, RB = DH * 2;
+  const float inv = X.l > 0.f ? 1.f / X.l : 0.f;
+#pragma unroll
+  for (int db = 0; db < X.NB; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int phys = (db * 4 + g) ^ (ln.n & (CH - 1));
+      u32x2 w = {pack_bf16x2(X.acc[db][g * 4] * inv, X.acc[db][g * 4 + 1] * inv),
+                 pack_bf16x2(X.acc[db][g * 4 + 2] * inv, X.acc[db][g * 4 + 3] * inv)};
+      *reinterpret_cast<MXA_LDS u32x2*>((MXA_LDS unsigned char*)wbuf + ln.n * RB + phys * 16 + ln.h * 8) = w;
+    }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+  for (int i = 0; i < 32 * CH / 64; ++i) {
+    const int idx = i * 64 + ln.lane, r = idx / CH, c = idx % CH;
+    const u32x4 val =
+        *reinterpret_cast<const MXA_LDS u32x4*>((MXA_LDS unsigned char*)wbuf + r * RB + ((c ^ (r & (CH - 1))) * 16));
+    const int row = row0 + r;
+    if (row < p.Sq) *reinterpret_cast<u32x4*>(o + int64_t(row) * p.o_stride + head * DH + c * 8) = val;
+  }
+}
+
 // ---------------- PP: 8 waves x 32 queries, ping-pong groups ----------------
 // Waves w and w + 4 share a SIMD. Group A (waves 0-3) and group B (waves 4-7)
 // run the same per-tile program offset by one period, so in every period one
@@ -398,9 +430,26 @@ __device__ __forceinline__ void store_partial(const QBlock<DH>& X, const BfSplit
 // waited for before its MFMA; config-2 shape 176 -> 146 us with the target stated).
 // The non-causal kernels keep the equivalent of __launch_bounds__(512, 1): the stated
 // target changes their schedule for the worse at D = 64 and not at all at D = 128.
+#ifdef MX_STAMPS
+// Timing probe (debug builds only): per work-group, the 100 MHz chip clock at kernel
+// entry, after the prologue, after the tile loop and after the store, plus HW_ID and
+// XCC_ID.
+__device__ uint64_t g_stamps[1 << 20];
+__device__ __forceinline__ void stamp(int slot) {
+  if (threadIdx.x == 0) {
+    uint64_t* d = g_stamps + size_t(blockIdx.x) * 8;
+    d[slot] = __builtin_amdgcn_s_memrealtime();
+    if (slot == 0) d[6] = (uint64_t(__builtin_amdgcn_s_getreg(0xF814)) << 32) | __builtin_amdgcn_s_getreg(0xF804);
+  }
+}
+#define MX_STAMP(i) stamp(i)
+#else
+#define MX_STAMP(i)
+#endif
+
 template <int DH, bool CAUSAL, bool SPLIT>
-__global__ void __attribute__((amdgpu_flat_work_group_size(CAUSAL ? 512 : 1, 512),
-                               amdgpu_waves_per_eu(CAUSAL ? 2 : 1, CAUSAL ? 2 : 8)))
+__global__ void __attribute__((amdgpu_flat_work_group_size(CAUSAL || DH == 128 ? 512 : 1, 512),
+                               amdgpu_waves_per_eu(CAUSAL || DH == 128 ? 2 : 1, CAUSAL || DH == 128 ? 2 : 8)))
 flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
               uint16_t* __restrict__ o, mx_attn_params p, float c, uint32_t qsign, BfSplit sp) {
   using Dm = Dims<DH>;
@@ -411,6 +460,7 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
   __shared__ __align__(16) unsigned char vb0[Dm::VTB];
   __shared__ __align__(16) unsigned char vb1[Dm::VTB];
   __shared__ uint64_t live_tiles[kMaxLiveTiles];
+  MX_STAMP(0);
   const Lane ln(c);
   const int wave = threadIdx.x >> 6;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -441,11 +491,16 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
     store_block(A, o, p, q0, head, ln);
     return;
   }
+  // 16-byte aligned mask: its loads go first and are folded after the tile and Q loads
+  const bool mask16 = p.kv_valid && (reinterpret_cast<uintptr_t>(p.kv_valid) & 15) == 0;
+  Live16 lv16{};
+  if (mask16) lv16 = live16_issue<NW>(p, nt, wave_u, ln.lane);
   load_tile<NW, false, DH>(k, tb, kb0, p, kvbase, wave_u, ta8);
   load_tile<NW, true, DH>(v, tb, vb0, p, kvbase, wave_u, ta8);
   if (nt > tb + 1) load_tile<NW, false, DH>(k, tb + 1, kb1, p, kvbase, wave_u, ta8);
   qblock_init(A, q, p, q0, head, ln, qsign);
-  build_live<NW, KT>(live_tiles, p, nt, wave, ln.lane);
+  if (mask16) live16_finish<NW>(live_tiles, lv16, p, nt, wave_u, ln.lane);
+  else build_live<NW, KT>(live_tiles, p, nt, wave, ln.lane);
 
   // MFMA period of tile t: P V(t) then S(t+1). S(t+1) on a stale buffer when
   // t + 1 == nt is harmless (never read). With LOAD, also the DMA of V(t+1) and
@@ -478,6 +533,7 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
 
   wait_vm_n<0>();
   __syncthreads();  // K(0), V(0), K(1) and the liveness bitmaps are visible
+  MX_STAMP(1);
   if (group_a) {    // period -1: S_A(0)
     scores(kb0, A, ln);
     sched_k<2 * Dm::NC, 0>();
@@ -509,8 +565,26 @@ flash_bf16_pp(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, co
     if (t + 1 < nt) tile(t + 1, kb0, vb1, kb1, vb0);
   }
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
-  if constexpr (SPLIT) store_partial(A, sp, su, part, wave * 32 + ln.n, ln);
-  else store_block(A, o, p, q0, head, ln);
+  MX_STAMP(2);
+  if constexpr (SPLIT) {
+    store_partial(A, sp, su, part, wave * 32 + ln.n, ln);
+  } else if constexpr (DH % 32 == 0) {
+    if ((reinterpret_cast<uintptr_t>(o) & 15) == 0 && (p.o_stride & 7) == 0) {
+      block_sync();  // every wave is done reading the K/V buffers
+      const int wb = wave_u >> 1;
+      unsigned char* buf = wb == 0 ? kb0 : wb == 1 ? kb1 : wb == 2 ? vb0 : vb1;
+      store_block_lds(A, o, p, q0, head, ln, buf + (wave_u & 1) * 32 * DH * 2);
+    } else {
+      store_block(A, o, p, q0, head, ln);
+    }
+  } else {
+    store_block(A, o, p, q0, head, ln);
+  }
+#ifdef MX_STAMPS
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  MX_STAMP(3);
+#endif
 }
 
 // Merge of the split units' parts: one thread per (query, 8 channels). With
@@ -727,3 +801,9 @@ hipError_t launch_flash_bf16(const uint16_t* q, const uint16_t* k, const uint16_
 }
 
 }  // namespace mxa
+
+#ifdef MX_STAMPS
+extern "C" int mx_debug_stamps(void* dst, size_t bytes) {
+  return int(hipMemcpyFromSymbol(dst, HIP_SYMBOL(mxa::g_stamps), bytes, 0, hipMemcpyDeviceToHost));
+}
+#endif
