@@ -239,24 +239,27 @@ def cpu_baseline_sage(q, k, v, mask, S, H, D, budget_s: float = 8.0) -> dict:
 
 BS_M, BS_N, BS_K = 8192, 12288, 4096  # the reference's quoted block-scaled GEMM shape (src/kernels/blockscale.h:2)
 BS_REF_TFLOPS = 152.0                 # its MXFP8 figure there (RTX 5060 Ti, cuBLASLt)
+BS_REF_TFLOPS_FP4 = 293.0             # its NVFP4 figure there (src/kernels/blockscale.h:2)
 
 
-def _blockscale_setup(dev):
-    """MXFP8 operands of the quoted shape: W [N, K] quantized once, activations X [M, K];
-    returns the GEMM call Y[M, N] = X W^T (bf16 out)."""
+def _blockscale_setup(dev, mode=None):
+    """Block-scaled operands of the quoted shape (MXFP8 unless `mode`): W [N, K] quantized
+    once, activations X [M, K]; returns the GEMM call Y[M, N] = X W^T (bf16 out)."""
     import torch
 
     from miroxen_amd.blockscale import QMat, QMode, gemm_blockscaled, qdata_bytes, qscale_bytes, quantize_blockscaled
+    mode = QMode.MXFP8 if mode is None else mode
     g = torch.Generator(device=dev).manual_seed(41)
     x = torch.randn(BS_M, BS_K, device=dev, generator=g).to(torch.bfloat16)
     w = (torch.randn(BS_N, BS_K, device=dev, generator=g) * 0.05).to(torch.bfloat16)
-    mk = lambda r: QMat(torch.empty(qdata_bytes(QMode.MXFP8, r, BS_K), dtype=torch.uint8, device=dev),
-                        torch.empty(qscale_bytes(QMode.MXFP8, r, BS_K), dtype=torch.uint8, device=dev))
+    mk = lambda r: QMat(torch.empty(qdata_bytes(mode, r, BS_K), dtype=torch.uint8, device=dev),
+                        torch.empty(qscale_bytes(mode, r, BS_K), dtype=torch.uint8, device=dev),
+                        torch.empty(4, dtype=torch.float32, device=dev))
     X, W = mk(BS_M), mk(BS_N)
-    quantize_blockscaled(QMode.MXFP8, w, BS_K, BS_N, BS_K, W)
-    quantize_blockscaled(QMode.MXFP8, x, BS_K, BS_M, BS_K, X)
+    quantize_blockscaled(mode, w, BS_K, BS_N, BS_K, W)
+    quantize_blockscaled(mode, x, BS_K, BS_M, BS_K, X)
     y = torch.empty(BS_M, BS_N, dtype=torch.bfloat16, device=dev)
-    return lambda: gemm_blockscaled(QMode.MXFP8, W, X, y, BS_N, BS_M, BS_N, BS_K)
+    return lambda: gemm_blockscaled(mode, W, X, y, BS_N, BS_M, BS_N, BS_K)
 
 
 def blockscale_cpu_baseline(budget_s: float = 8.0) -> dict:
@@ -306,6 +309,25 @@ def blockscale_leg(dev, steps: int, warmup: int, warm_s: float) -> dict:
         mq = _time(lambda: quantize_blockscaled(QMode.MXFP8, x, K, M, K, qm), steps, warmup, warm_s)
         gbs = (2.0 * M * K + M * K) / (mq * 1e-3) / 1e9
         quant[f"{M}x{K}"] = {"us": round(mq * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
+    # NVFP4: e2m1 data, e4m3 scale per 16, per-tensor amax; dequantized exactly to f16 in
+    # the kernel and multiplied on the f16 MFMA (peak 2.5 PFLOP/s dense)
+    run4 = _blockscale_setup(dev, QMode.NVFP4)
+    ms4 = _time(run4, n, warmup, warm_s)
+    tf4 = 2.0 * BS_M * BS_N * BS_K / (ms4 * 1e-3) / 1e12
+    quant4 = {}
+    for (M, K) in ((4096, 4096), (4096, 12288)):
+        x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+        qm = QMat(torch.empty(qdata_bytes(QMode.NVFP4, M, K), dtype=torch.uint8, device=dev),
+                  torch.empty(qscale_bytes(QMode.NVFP4, M, K), dtype=torch.uint8, device=dev),
+                  torch.empty(4, dtype=torch.float32, device=dev))
+        mq = _time(lambda: quantize_blockscaled(QMode.NVFP4, x, K, M, K, qm), steps, warmup, warm_s)
+        gbs = (2.0 * M * K + M * K / 2) / (mq * 1e-3) / 1e9  # counted as the reference: bf16 in + fp4 out
+        quant4[f"{M}x{K}"] = {"us": round(mq * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)}
+    nvfp4 = {"ms": round(ms4, 4), "tflops": round(tf4, 1), "reference_published_tflops": BS_REF_TFLOPS_FP4,
+             "dtype": "e2m1 x e2m1 with e4m3 scales per 16, dequantized to f16 (exact), fp32 accumulate",
+             "roofline": {"bound": "mfma", "achieved": round(tf4, 1), "peak": PEAK_BF16, "unit": "TFLOP/s",
+                          "frac": round(tf4 / PEAK_BF16, 4), "traffic": _traffic("nvfp4_gemm")},
+             "quantize": quant4}
     return {
         "workload": f"MXFP8 GEMM Y[M,N] = X[M,K] W[N,K]^T, M={BS_M} N={BS_N} K={BS_K}, bf16 out",
         "steps": n, "ms": round(ms, 4), "tflops": round(tf, 1),
@@ -314,6 +336,7 @@ def blockscale_leg(dev, steps: int, warmup: int, warm_s: float) -> dict:
         "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_FP8, "unit": "TFLOP/s",
                      "frac": round(tf / PEAK_FP8, 4), "traffic": _traffic("mxfp8_gemm")},
         "quantize": quant,
+        "nvfp4": nvfp4,
     }
 
 
@@ -331,8 +354,9 @@ def _only(which: str, n: int) -> int:
             b.copy_(a)
         torch.cuda.synchronize()
         return 0
-    if which == "blockscale":
-        run = _blockscale_setup(dev)
+    if which in ("blockscale", "nvfp4"):
+        from miroxen_amd.blockscale import QMode
+        run = _blockscale_setup(dev, QMode.NVFP4 if which == "nvfp4" else None)
         for _ in range(n):
             run()
         torch.cuda.synchronize()
@@ -383,7 +407,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--skip-large", action="store_true", help="skip configs 4 and 5 (S=12544, S=32760)")
     ap.add_argument("--no-blockscale", action="store_true", help="skip the MXFP8 block-scaled GEMM leg")
-    ap.add_argument("--only", choices=["bf16", "sage", "sage_e2e", "prologue", "fused", "copy", "blockscale"],
+    ap.add_argument("--only", choices=["bf16", "sage", "sage_e2e", "prologue", "fused", "copy", "blockscale", "nvfp4"],
                     help="profiling driver: run just this kernel --steps times (no warm-up, no JSON); "
                          "'copy' is a 256 MiB device copy for calibrating HBM byte counters")
     args = ap.parse_args()

@@ -62,7 +62,7 @@ inline void quantize_blockscaled(QMode m, const __hip_bfloat16* x, int64_t ldx, 
 
 inline void gemm_blockscaled(hipStream_t s, QMode m, const QMat& W, const QMat& X, __hip_bfloat16* Y, int64_t ldy,
                              int64_t M, int64_t N, int64_t K, float beta = 0.f) {
-  detail::bs_check(mx_gemm_blockscaled(int(m), W.q, W.sf, X.q, X.sf, Y, ldy, M, N, K, beta, s));
+  detail::bs_check(mx_gemm_blockscaled(int(m), W.q, W.sf, W.amax, X.q, X.sf, X.amax, Y, ldy, M, N, K, beta, s));
 }
 
 // The reference's signature (src/kernels/blockscale.h:34-35): the context's stream.

@@ -208,28 +208,36 @@ int mx_flash_attn_fp8_norm_rope(const void* q, const void* k, const void* v, voi
  * Reference: src/kernels/blockscale.h:12-37 (QMode, QMat, qmode_supported,
  * qdata_bytes, qscale_bytes, quantize_blockscaled, gemm_blockscaled; cuBLASLt in
  * blockscale.cu:134-216). MX_QMODE_MXFP8: e4m3 data, one UE8M0 (power-of-two)
- * scale per 32 K values, on gfx950's scaled MFMA. MX_QMODE_NVFP4 (e4m3 scales per
- * 16 values + a per-tensor scale) has no gfx950 scaled-MFMA form: qmode_supported
- * reports 0 and the caller keeps BF16, as the reference does on cards without it.
+ * scale per 32 K values, on gfx950's scaled MFMA. MX_QMODE_NVFP4: e2m1 data (two
+ * per byte, low nibble first), one e4m3 scale per 16 K values and a per-tensor amax
+ * (device float, written by quantize_blockscaled); gfx950's scaled MFMA has no
+ * e4m3-per-16 form, so the GEMM dequantizes exactly to f16 in registers and runs
+ * the f16 MFMA with fp32 accumulation and alpha = (amaxW / 2688) (amaxX / 2688).
  * Scale layout: the reference's 128x4 interleave (blockscale.cu:82, decoded by
  * tests/blockscale_test.cpp:15-17): scale (r, kb) at byte (r/128)*kbp*128 +
- * (kb/4)*512 + (r%32)*16 + ((r%128)/32)*4 + kb%4, kbp = K/32 rounded up to 4, rows
- * padded to 128; padding bytes hold 127 (1.0). */
+ * (kb/4)*512 + (r%32)*16 + ((r%128)/32)*4 + kb%4, kbp = K/vec rounded up to 4
+ * (vec 32 MXFP8, 16 NVFP4), rows padded to 128; padding bytes hold 127 (1.0) for
+ * MXFP8 and 0 for NVFP4. */
 enum { MX_QMODE_BF16 = 0, MX_QMODE_MXFP8 = 1, MX_QMODE_NVFP4 = 2 };
 int mx_qmode_supported(int mode, int device, int* supported);
 size_t mx_qdata_bytes(int mode, int64_t rows, int64_t K);
 size_t mx_qscale_bytes(int mode, int64_t rows, int64_t K);
 /* Reference quantize_blockscaled (blockscale.cu:113-131): x [rows, K] bf16 with row
- * stride ldx -> q [rows, K] e4m3 (dense) and sf. K % 32 == 0, ldx % 8 == 0, x 16-byte
- * aligned (reference MX_CHECK). amax is unused for MXFP8 (may be NULL). */
+ * stride ldx -> q (MXFP8: [rows, K] e4m3, 16-byte aligned; NVFP4: [rows, K/2] e2m1
+ * pairs, 8-byte aligned) and sf. K % 32 == 0, ldx % 8 == 0, x 16-byte aligned
+ * (reference MX_CHECK). amax: NVFP4's per-tensor max |x| (device float, required);
+ * unused for MXFP8 (may be NULL). */
 int mx_quantize_blockscaled(int mode, const void* x, int64_t ldx, int64_t rows, int64_t K, void* q, void* sf,
                             float* amax, void* stream);
 /* Reference gemm_blockscaled (blockscale.cu:134-216): Y[M, N] (bf16, row stride ldy)
  * = X[M, K] W[N, K]^T (+ Y when beta == 1), both quantized with the same mode; beta
- * must be 0 or 1. The reference's Ctx argument (cuBLASLt handle and workspace)
- * becomes the stream: this kernel needs neither. */
-int mx_gemm_blockscaled(int mode, const void* wq, const void* wsf, const void* xq, const void* xsf, void* y,
-                        int64_t ldy, int64_t M, int64_t N, int64_t K, float beta, void* stream);
+ * must be 0 or 1. The QMat arguments are passed field by field (data, scales, amax);
+ * wamax / xamax are the NVFP4 per-tensor amax values (required for NVFP4, ignored
+ * for MXFP8). The reference's Ctx argument (cuBLASLt handle and workspace) becomes
+ * the stream: these kernels need neither. */
+int mx_gemm_blockscaled(int mode, const void* wq, const void* wsf, const float* wamax, const void* xq, const void* xsf,
+                        const float* xamax, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, float beta,
+                        void* stream);
 
 #ifdef __cplusplus
 }

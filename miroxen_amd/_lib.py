@@ -85,8 +85,8 @@ def load():
         "mx_qscale_bytes": ([ctypes.c_int, ctypes.c_int64, ctypes.c_int64], ctypes.c_size_t),
         "mx_quantize_blockscaled": ([ctypes.c_int, vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, vp, vp, vp,
                                      vp], ctypes.c_int),
-        "mx_gemm_blockscaled": ([ctypes.c_int, vp, vp, vp, vp, vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
-                                 ctypes.c_int64, ctypes.c_float, vp], ctypes.c_int),
+        "mx_gemm_blockscaled": ([ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, ctypes.c_int64, ctypes.c_int64,
+                                 ctypes.c_int64, ctypes.c_int64, ctypes.c_float, vp], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

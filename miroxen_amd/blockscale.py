@@ -2,8 +2,9 @@
 
 QMode / QMat / qmode_name / parse_qmode / qmode_supported / qdata_bytes / qscale_bytes /
 quantize_blockscaled / gemm_blockscaled with the reference's names, argument meaning and
-errors (RuntimeError for its MX_CHECK). MXFP8 runs on gfx950's scaled MFMA; NVFP4 is
-reported unsupported (callers keep BF16, as the reference does without sm_100).
+errors (RuntimeError for its MX_CHECK). MXFP8 runs on gfx950's scaled MFMA; NVFP4 (e2m1
+with e4m3 scales per 16 and a per-tensor amax) is dequantized exactly to f16 inside the
+GEMM and runs on the f16 MFMA.
 """
 from __future__ import annotations
 
@@ -69,5 +70,6 @@ def quantize_blockscaled(m: QMode, x, ldx: int, rows: int, K: int, out: QMat, st
 def gemm_blockscaled(m: QMode, W: QMat, X: QMat, Y, ldy: int, M: int, N: int, K: int, beta: float = 0.0,
                      stream=None) -> None:
     """Reference gemm_blockscaled (blockscale.cu:134-216): Y[M, N] = X W^T (+ Y if beta == 1)."""
-    _lib.check(_lib.load().mx_gemm_blockscaled(int(m), _addr(W.q), _addr(W.sf), _addr(X.q), _addr(X.sf), _addr(Y),
-                                               ldy, M, N, K, beta, _stream(stream)))
+    _lib.check(_lib.load().mx_gemm_blockscaled(int(m), _addr(W.q), _addr(W.sf), _addr(W.amax), _addr(X.q),
+                                               _addr(X.sf), _addr(X.amax), _addr(Y), ldy, M, N, K, beta,
+                                               _stream(stream)))

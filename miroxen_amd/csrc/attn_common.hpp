@@ -207,4 +207,21 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
   return x * q + (x < r ? x : r) + local;
 }
 
+#ifdef MX_STAMPS
+// Timing probe (debug builds only, one array per translation unit): per work-group,
+// slots 0-3 take the 100 MHz chip clock at points the kernel chooses, slot 6 HW_ID
+// and XCC_ID.
+static __device__ uint64_t g_stamps[1 << 20];
+__device__ __forceinline__ void stamp(int slot) {
+  if (threadIdx.x == 0) {
+    uint64_t* d = g_stamps + size_t(blockIdx.x) * 8;
+    d[slot] = __builtin_amdgcn_s_memrealtime();
+    if (slot == 0) d[6] = (uint64_t(__builtin_amdgcn_s_getreg(0xF814)) << 32) | __builtin_amdgcn_s_getreg(0xF804);
+  }
+}
+#define MX_STAMP(i) stamp(i)
+#else
+#define MX_STAMP(i)
+#endif
+
 }  // namespace mxa

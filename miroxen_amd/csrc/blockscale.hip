@@ -130,6 +130,65 @@ __device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rs, const OpAdd
   }
 }
 
+// Epilogue through LDS: the 256 x 256 bf16 Y tile (row m = 512 B of n) fills the
+// stage buffers. Lane (m = lane % 32 of block j, h = lane / 32) holds n = 8g + 4h +
+// (0..3) of block i; 16-byte chunk q of row m sits at q ^ (m % 16), so the 8-byte
+// writes and the 16-byte row reads are free of bank conflicts, and each row goes out
+// as coalesced 16-byte stores. ALPHA: Y = alpha * C (+ Y).
+template <bool ALPHA>
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], unsigned char* lds, uint16_t* __restrict__ y,
+                                           int64_t ldy, int M, int N, int m0, int n0, int wm, int wn, int lane,
+                                           int beta, float alpha) {
+  const int n = lane & 31, h = lane >> 5;
+  block_sync();  // every wave is done with the operand buffers
+  {
+    const int xs = lane & 15;  // m % 16 (wm and 32 j are multiples of 16)
+    unsigned char* wp = lds + (wm + n) * 512 + 8 * h + wn * 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int cs = ((4 * i + g) ^ xs) << 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x16& c = acc[i][j];
+          float v[4] = {c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
+          if constexpr (ALPHA) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] *= alpha;
+          }
+          if (beta) {  // Y += C with one rounding: add the old values in fp32 here
+            const int m = m0 + wm + 32 * j + n, nb = n0 + wn + 32 * i + 8 * g + 4 * h;
+            if (m < M) {
+              const uint16_t* p = y + int64_t(m) * ldy + nb;
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (nb + e < N) v[e] += bf2f(p[e]);
+            }
+          }
+          *reinterpret_cast<u32x2*>(wp + j * 32 * 512 + cs) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        }
+      }
+  }
+  block_sync();
+  const bool vec = (reinterpret_cast<uintptr_t>(y) & 15) == 0 && ldy % 8 == 0;
+  const int c = threadIdx.x & 31, nn = n0 + 8 * c;
+#pragma unroll 4
+  for (int it = 0; it < 32; ++it) {
+    const int r = it * 8 + (threadIdx.x >> 5), m = m0 + r;
+    if (m >= M) break;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + r * 512 + ((c ^ (r & 15)) << 4));
+    uint16_t* p = y + int64_t(m) * ldy + nn;
+    if (vec && nn + 7 < N) {
+      *reinterpret_cast<u32x4*>(p) = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (nn + e < N) p[e] = uint16_t(v[e >> 1] >> ((e & 1) * 16));
+    }
+  }
+}
+
 __global__ void __launch_bounds__(256, 1)
 mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, const uint8_t* __restrict__ xq,
            const uint8_t* __restrict__ xsf, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int beta,
@@ -309,54 +368,232 @@ mxfp8_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, cons
   }
   wait_vm();  // no LDS-DMA may land after the work-group ends
 
-  // epilogue through LDS: the 256 x 256 bf16 Y tile (row m = 512 B of n) fills
-  // the stage buffers. Lane (m = lane % 32 of block j, h = lane / 32) holds n =
-  // 8g + 4h + (0..3) of block i; 16-byte chunk q of row m sits at q ^ (m % 16), so
-  // the 8-byte writes and the 16-byte row reads are free of bank conflicts, and
-  // each row goes out as coalesced 16-byte stores.
-  block_sync();  // every wave is done with the operand buffers
-  {
-    const int xs = lane & 15;  // m % 16 (wm and 32 j are multiples of 16)
-    unsigned char* wp = lds + (wm + n) * 512 + 8 * h + wn * 2;
+  store_tile<false>(acc, lds, y, ldy, M, N, m0, n0, wm, wn, lane, beta, 1.f);
+}
+
+
+// ---------------- NVFP4 ----------------
+// Format (the reference's NVFP4, blockscale.cu:36-93): e2m1 data, two per byte (the
+// lower-index value in the low nibble), one e4m3 scale per 16 consecutive K values of
+// a row (the same 128 x 4 interleave with K/16 blocks, padding bytes 0, as the
+// reference's memset), and a per-tensor amax: g = amax / (6 * 448), block scale
+// se = e4m3(bmax / (6 g)), codes e2m1(x / (se g)). The GEMM returns
+// alpha * sum (e2m1 se)_X (e2m1 se)_W with alpha = gW gX.
+constexpr int kFp4Block = 16;
+constexpr float kFp4Range = 6.f * 448.f;
+
+__global__ void nvfp4_amax_init(float* amax) {
+  if (threadIdx.x == 0) *amax = 0.f;
+}
+
+// max |x| of the tensor (reference amax_kernel :45-67): a 1024-thread work-group per
+// range of rows, four 16-byte loads in flight per thread, a wave max, the work-group
+// max through LDS, one atomic max per work-group on the value's bits (non-negative
+// floats order as integers). At most 256 work-groups: atomics on one address
+// serialise (one per wave cost ~40 us at 4096 x 4096).
+__global__ void __launch_bounds__(1024) nvfp4_amax(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
+                                                   int64_t K, float* amax) {
+  const int64_t nv = K / 8;
+  const int64_t per = (rows + gridDim.x - 1) / gridDim.x;
+  const int64_t r0 = int64_t(blockIdx.x) * per, r1 = r0 + per < rows ? r0 + per : rows;
+  const int64_t n = r1 > r0 ? (r1 - r0) * nv : 0;
+  float m = 0.f;
+  for (int64_t i0 = threadIdx.x; i0 < n; i0 += 4 * 1024) {
+    u32x4 u[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int k = 0; k < 4; ++k) {
+      const int64_t i = i0 + k * 1024;
+      const int64_t r = r0 + i / nv, j = i - (i / nv) * nv;
+      u[k] = i < n ? *reinterpret_cast<const u32x4*>(x + r * ldx + 8 * j) : u32x4{0, 0, 0, 0};
+    }
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int cs = ((4 * i + g) ^ xs) << 4;
+    for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f32x16& c = acc[i][j];
-          float v[4] = {c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
-          if (beta) {  // Y += C with one rounding: add the old values in fp32 here
-            const int m = m0 + wm + 32 * j + n, nb = n0 + wn + 32 * i + 8 * g + 4 * h;
-            if (m < M) {
-              const uint16_t* p = y + int64_t(m) * ldy + nb;
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (nb + e < N) v[e] += bf2f(p[e]);
-            }
-          }
-          *reinterpret_cast<u32x2*>(wp + j * 32 * 512 + cs) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        }
-      }
+      for (int t = 0; t < 8; ++t) m = fmaxf(m, fabsf(bf2f(uint16_t(u[k][t >> 1] >> ((t & 1) * 16)))));
   }
-  block_sync();
-  const bool vec = (reinterpret_cast<uintptr_t>(y) & 15) == 0 && ldy % 8 == 0;
-  const int c = threadIdx.x & 31, nn = n0 + 8 * c;
-#pragma unroll 4
-  for (int it = 0; it < 32; ++it) {
-    const int r = it * 8 + (threadIdx.x >> 5), m = m0 + r;
-    if (m >= M) break;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + r * 512 + ((c ^ (r & 15)) << 4));
-    uint16_t* p = y + int64_t(m) * ldy + nn;
-    if (vec && nn + 7 < N) {
-      *reinterpret_cast<u32x4*>(p) = v;
-    } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (nn + e < N) p[e] = uint16_t(v[e >> 1] >> ((e & 1) * 16));
+  for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  __shared__ float wmax[16];
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < 16; ++w) m = fmaxf(m, wmax[w]);
+    atomicMax(reinterpret_cast<int*>(amax), __float_as_int(m));
+  }
+}
+
+// One thread per 16-value block of a row (reference quant_kernel NVFP4 branch :76-93);
+// padding scale bytes get 0.
+__global__ void __launch_bounds__(256) nvfp4_quant(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
+                                                   int64_t K, uint8_t* __restrict__ q, uint8_t* __restrict__ sf,
+                                                   const float* __restrict__ amax, int64_t kbp, int64_t rows_pad) {
+  const int64_t nkb = K / kFp4Block;
+  const int64_t id = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (id >= rows_pad * kbp) return;
+  const int64_t r = id / kbp, kb = id % kbp;
+  const int64_t so = (r / 128) * kbp * 128 + (kb / 4) * 512 + (r % 32) * 16 + (r % 128) / 32 * 4 + kb % 4;
+  if (r >= rows || kb >= nkb) {
+    sf[so] = 0;
+    return;
+  }
+  const uint16_t* src = x + r * ldx + kb * kFp4Block;
+  float v[16];
+  float bmax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const u32x4 u = *reinterpret_cast<const u32x4*>(src + 8 * j);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      v[8 * j + t] = bf2f(uint16_t(u[t >> 1] >> ((t & 1) * 16)));
+      bmax = fmaxf(bmax, fabsf(v[8 * j + t]));
     }
   }
+  const float a = *amax;
+  const float g = a > 0.f ? a / kFp4Range : 1.f;
+  const float inv6g = 1.f / (6.f * g);
+  // e4m3 of bmax / (6 g), saturating: clamp to 448, then round to nearest even
+  const float t = __builtin_fminf(bmax * inv6g, 448.f);
+  const uint32_t se = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(t, t, 0, false)) & 0xffu;
+  const float sd = __builtin_amdgcn_cvt_f32_fp8(int(se), 0) * g;
+  const float inv = sd > 0.f ? 1.f / sd : 0.f;
+  // e2m1 codes: v_cvt_scalef32_pk_fp4_f32 (scale 1) rounds to the nearest magnitude of
+  // {0, 0.5, 1, 1.5, 2, 3, 4, 6} with ties to the even code, saturates at 6 and sets the
+  // sign bit for negative values: the reference's threshold sum (:38-42), checked on
+  // the device against it over 2M value pairs (every midpoint +-1 ulp, -0, saturation);
+  // two values per byte, the lower-index one in the low nibble
+  u32x2 w = {0u, 0u};
+  static_for<8>([&](auto jc) __attribute__((always_inline)) {
+    constexpr int j = decltype(jc)::value;
+    w[j >> 2] = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w[j >> 2], v[2 * j] * inv, v[2 * j + 1] * inv, 1.f, j & 3);
+  });
+  *reinterpret_cast<u32x2*>(q + (r * K + kb * kFp4Block) / 2) = w;
+  sf[so] = uint8_t(se);
+}
+
+// NVFP4 GEMM: the MXFP8 kernel's tiling (256 n x 256 m per 4-wave work-group, 128 x 128
+// per wave, 256 fp32 accumulators in AGPRs, K stages of 128 bytes = 256 values DMA'd
+// into LDS with the same swizzle, XCD-grouped tile order, LDS epilogue), but the raw e2m1
+// data is dequantized in registers and multiplied on the f16 MFMA (32x32x16). gfx950's
+// scaled MFMA takes one power-of-two scale per 32 values, NVFP4 an e4m3 scale per 16;
+// the product of an e2m1 value and an e4m3 scale has at most 5 significant bits, so
+// e2m1 -> f16 (v_cvt_scalef32_pk_f16_fp4, scale 1) times the block scale in f16
+// (v_pk_mul_f16) is exact, as are the MFMA's f16 products; accumulation is fp32, and
+// alpha = gW gX scales the tile in the epilogue.
+//
+// Operand layout: the MFMA sums its 16 K values in any order, so the two lane halves
+// take different 16-value blocks: for 32-value chunk c of a stage, lane half h of row
+// r reads the 8 bytes of block 2c + h (one ds_read_b64) and feeds values 0-7 of it to
+// MFMA step 2c and values 8-15 to step 2c + 1; W and X use the same assignment, so
+// every product pairs the same K. One e4m3 scale per lane per chunk and operand block.
+using f16x2 = __attribute__((ext_vector_type(2))) _Float16;
+using f16x8 = __attribute__((ext_vector_type(8))) _Float16;
+
+__device__ __forceinline__ f16x8 fp4x8_to_f16(uint32_t d, f16x2 s) {
+  const f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.f, 0) * s;
+  const f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.f, 1) * s;
+  const f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.f, 2) * s;
+  const f16x2 e = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(d, 1.f, 3) * s;
+  return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], e[0], e[1]};
+}
+
+__global__ void __launch_bounds__(256, 1)
+nvfp4_gemm(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ wsf, const float* __restrict__ wamax,
+           const uint8_t* __restrict__ xq, const uint8_t* __restrict__ xsf, const float* __restrict__ xamax,
+           uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int beta, int ntn, int ntm) {
+  __shared__ __align__(16) unsigned char lds[4 * kStageB];
+  // stage buffers: operand W at lds + bi * kStageB, operand X at lds + (2 + bi) * kStageB
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int gsz = kGroupM * ntn, grp = L / gsz, fm = grp * kGroupM;
+  const int gm = min(ntm - fm, kGroupM), li = L - grp * gsz;
+  const int tm = fm + li % gm, tn = li / gm;
+  const int n0 = tn * kTile, m0 = tm * kTile;
+  const int wn = (wave & 1) * 128, wm = (wave >> 1) * 128;
+  const int RB = K / 2;                                  // bytes per row
+  const int kbp = int(pad_up(K / kFp4Block, 4));
+  const int nst = (RB + kStage - 1) / kStage;            // stages of 256 values
+
+  const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wq + int64_t(n0) * RB, uint32_t(int64_t(N - n0) * RB));
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xq + int64_t(m0) * RB, uint32_t(int64_t(M - m0) * RB));
+  const OpAddr oa = op_addr(RB, lane, wave_u);
+  // Scales: a wave's 128 rows are one 128-row band; lane n's bytes for row blocks b =
+  // 0..3 (r % 32 = n, (r % 128) / 32 = b) and K blocks 4t..4t+3 are the 16 bytes at
+  // band + t 512 + 16 n (word b, byte kb % 4). A stage's 16 blocks: 4 loads per operand.
+  const int n = lane & 31, h = lane >> 5;
+  const __amdgpu_buffer_rsrc_t rsw = buf_rsrc(wsf, uint32_t(pad_up(N, 128) * kbp));
+  const __amdgpu_buffer_rsrc_t rsx = buf_rsrc(xsf, uint32_t(pad_up(M, 128) * kbp));
+  const uint32_t sw_off = uint32_t((n0 + wn) / 128) * uint32_t(kbp) * 128u + uint32_t(16 * n);
+  const uint32_t sx_off = uint32_t((m0 + wm) / 128) * uint32_t(kbp) * 128u + uint32_t(16 * n);
+  auto fetch = [&](int st, int bi, u32x4 (&sa)[4], u32x4 (&sb)[4]) __attribute__((always_inline)) {
+    dma_stage(rw, oa, RB, st * kStage, lds + bi * kStageB, wave_u);
+    dma_stage(rx, oa, RB, st * kStage, lds + (2 + bi) * kStageB, wave_u);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      sa[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsw, sw_off + uint32_t((4 * st + t) * 512), 0, 0));
+      sb[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsx, sx_off + uint32_t((4 * st + t) * 512), 0, 0));
+    }
+  };
+  // LDS read address of (row block b, chunk c): row (w* + 32 b + n), logical 16-byte
+  // chunk c at physical c ^ ((row >> 1) & 7), this half's 8 bytes
+  const int x = (n >> 1) & 7;
+  const int abase = (wn + n) * kStage + 8 * h, bbase = (wm + n) * kStage + 8 * h;
+  // the block scale of (row block b, chunk c) in f16, both halves of the pair
+  auto scale_of = [&](const u32x4 (&sw)[4], int b, int c) __attribute__((always_inline)) -> f16x2 {
+    const uint32_t byte = (sw[c >> 1][b] >> (8 * (2 * (c & 1) + h))) & 0xffu;
+    const float f = __builtin_amdgcn_cvt_f32_fp8(int(byte), 0);
+    return __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(f, f));
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[i][j] = f32x16{};
+      asm volatile("" : "+a"(acc[i][j]));
+    }
+
+  u32x4 sa[4], sb[4], na[4], nb[4];
+  fetch(0, 0, na, nb);
+  for (int st = 0; st < nst; ++st) {
+    const int bi = st & 1;
+    wait_vm();     // this wave's DMA of stage st and its scale words landed ...
+    block_sync();  // ... for every wave, and every wave is done with stage st - 1
+#pragma unroll
+    for (int t = 0; t < 4; ++t) sa[t] = na[t], sb[t] = nb[t];
+    if (st + 1 < nst) fetch(st + 1, bi ^ 1, na, nb);
+    const unsigned char* ca = lds + bi * kStageB;
+    const unsigned char* cb = lds + (2 + bi) * kStageB;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      u32x2 ra[4], rb[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int co = ((c ^ x) << 4) + b * 32 * kStage;
+        ra[b] = *reinterpret_cast<const u32x2*>(ca + abase + co);
+        rb[b] = *reinterpret_cast<const u32x2*>(cb + bbase + co);
+      }
+      f16x2 psa[4], psb[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) psa[b] = scale_of(sa, b, c), psb[b] = scale_of(sb, b, c);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        f16x8 av[4], bv[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) av[b] = fp4x8_to_f16(ra[b][u], psa[b]), bv[b] = fp4x8_to_f16(rb[b][u], psb[b]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+  wait_vm();  // no LDS-DMA may land after the work-group ends
+  const float aw = *wamax, ax = *xamax;
+  const float alpha = (aw > 0.f ? aw / kFp4Range : 1.f) * (ax > 0.f ? ax / kFp4Range : 1.f);
+  store_tile<true>(acc, lds, y, ldy, M, N, m0, n0, wm, wn, lane, beta, alpha);
 }
 
 }  // namespace
@@ -381,6 +618,31 @@ hipError_t launch_mxfp8_gemm(const uint8_t* wq, const uint8_t* wsf, const uint8_
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL(mxfp8_gemm, dim3(unsigned(blocks)), dim3(256), 0, s, wq, wsf, xq, xsf, y, ldy, M, N, K, beta,
                      ntn, ntm);
+  return hipGetLastError();
+}
+
+hipError_t launch_nvfp4_quant(const uint16_t* x, int64_t ldx, int64_t rows, int64_t K, uint8_t* q, uint8_t* sf,
+                              float* amax, hipStream_t s) {
+  const int64_t kbp = pad_up(K / kFp4Block, 4), rp = pad_up(rows, 128);
+  const int64_t blocks = (rp * kbp + 255) / 256;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(nvfp4_amax_init, dim3(1), dim3(64), 0, s, amax);
+  hipLaunchKernelGGL(nvfp4_amax, dim3(unsigned(rows < 256 ? rows : 256)), dim3(1024), 0, s, x, ldx, rows, K, amax);
+  hipLaunchKernelGGL(nvfp4_quant, dim3(unsigned(blocks)), dim3(256), 0, s, x, ldx, rows, K, q, sf,
+                     (const float*)amax, kbp, rp);
+  return hipGetLastError();
+}
+
+// Preconditions (checked by the caller): K % 32 == 0, (N + 255) / 256 * 256 * K / 2 < 2^31,
+// same for M; beta 0 or 1; the amax pointers are device floats written by the quantizer.
+hipError_t launch_nvfp4_gemm(const uint8_t* wq, const uint8_t* wsf, const float* wamax, const uint8_t* xq,
+                             const uint8_t* xsf, const float* xamax, uint16_t* y, int64_t ldy, int M, int N, int K,
+                             int beta, hipStream_t s) {
+  const int ntn = (N + kTile - 1) / kTile, ntm = (M + kTile - 1) / kTile;
+  const int64_t blocks = int64_t(ntn) * ntm;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(nvfp4_gemm, dim3(unsigned(blocks)), dim3(256), 0, s, wq, wsf, wamax, xq, xsf, xamax, y, ldy, M,
+                     N, K, beta, ntn, ntm);
   return hipGetLastError();
 }
 

@@ -32,6 +32,9 @@ size_t mx_qscale_size(int64_t rows, int64_t K);
 hipError_t launch_mxfp8_quant(const uint16_t*, int64_t, int64_t, int64_t, uint8_t*, uint8_t*, hipStream_t);
 hipError_t launch_mxfp8_gemm(const uint8_t*, const uint8_t*, const uint8_t*, const uint8_t*, uint16_t*, int64_t, int,
                              int, int, int, hipStream_t);
+hipError_t launch_nvfp4_quant(const uint16_t*, int64_t, int64_t, int64_t, uint8_t*, uint8_t*, float*, hipStream_t);
+hipError_t launch_nvfp4_gemm(const uint8_t*, const uint8_t*, const float*, const uint8_t*, const uint8_t*, const float*,
+                             uint16_t*, int64_t, int, int, int, int, hipStream_t);
 }  // namespace mxa
 
 namespace {
@@ -445,7 +448,7 @@ int mx_qmode_supported(int mode, int device, int* supported) {
   hipError_t e = hipGetDeviceCount(&count);
   if (e != hipSuccess) return hip_status(e, "qmode_supported");
   if (device < 0 || device >= count) return fail(MX_E_INVALID, "qmode_supported: no device %d", device);
-  *supported = mode == MX_QMODE_MXFP8 && device_is_gfx950(device) ? 1 : 0;
+  *supported = device_is_gfx950(device) ? 1 : 0;  // MXFP8 and NVFP4
   return MX_OK;
 }
 
@@ -462,25 +465,36 @@ size_t mx_qscale_bytes(int mode, int64_t rows, int64_t K) {
 
 int mx_quantize_blockscaled(int mode, const void* x, int64_t ldx, int64_t rows, int64_t K, void* q, void* sf,
                             float* amax, void* stream) {
-  (void)amax;
   if (mode == MX_QMODE_BF16) return fail(MX_E_INVALID, "quantize_blockscaled: bf16 is not a quantized mode");
-  if (mode != MX_QMODE_MXFP8) return fail(MX_E_UNSUPPORTED, "quantize_blockscaled: only MXFP8 on gfx950");
+  if (mode != MX_QMODE_MXFP8 && mode != MX_QMODE_NVFP4)
+    return fail(MX_E_INVALID, "quantize_blockscaled: unknown mode %d", mode);
   // reference MX_CHECK, blockscale.cu:116
   if (!(K % 32 == 0 && ldx % 8 == 0 && aligned(x, 16)))
     return fail(MX_E_INVALID, "quantize_blockscaled: need K%%32==0, ldx%%8==0, 16B-aligned input");
   if (rows == 0) return MX_OK;
-  if (rows < 0 || K <= 0 || ldx < K || !x || !q || !sf || !aligned(q, 16))
+  if (rows < 0 || K <= 0 || ldx < K || !x || !q || !sf || !aligned(q, mode == MX_QMODE_NVFP4 ? 8 : 16))
     return fail(MX_E_INVALID, "quantize_blockscaled: bad tensor arguments");
+  if (mode == MX_QMODE_NVFP4) {
+    if (!amax || !aligned(amax, 4)) return fail(MX_E_INVALID, "quantize_blockscaled: NVFP4 needs the amax pointer");
+    return hip_status(mxa::launch_nvfp4_quant(static_cast<const uint16_t*>(x), ldx, rows, K, static_cast<uint8_t*>(q),
+                                              static_cast<uint8_t*>(sf), amax, static_cast<hipStream_t>(stream)),
+                      "quantize_blockscaled");
+  }
   return hip_status(mxa::launch_mxfp8_quant(static_cast<const uint16_t*>(x), ldx, rows, K, static_cast<uint8_t*>(q),
                                             static_cast<uint8_t*>(sf), static_cast<hipStream_t>(stream)),
                     "quantize_blockscaled");
 }
 
-int mx_gemm_blockscaled(int mode, const void* wq, const void* wsf, const void* xq, const void* xsf, void* y,
-                        int64_t ldy, int64_t M, int64_t N, int64_t K, float beta, void* stream) {
+int mx_gemm_blockscaled(int mode, const void* wq, const void* wsf, const float* wamax, const void* xq, const void* xsf,
+                        const float* xamax, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, float beta,
+                        void* stream) {
   if (M == 0 || N == 0) return MX_OK;  // reference :136
   if (!(beta == 0.f || beta == 1.f)) return fail(MX_E_INVALID, "gemm_blockscaled: beta must be 0 or 1");
-  if (mode != MX_QMODE_MXFP8) return fail(MX_E_UNSUPPORTED, "gemm_blockscaled: only MXFP8 on gfx950");
+  if (mode != MX_QMODE_MXFP8 && mode != MX_QMODE_NVFP4)
+    return fail(MX_E_INVALID, "gemm_blockscaled: %s", mode == MX_QMODE_BF16 ? "bf16 is not a quantized mode"
+                                                                           : "unknown mode");
+  if (mode == MX_QMODE_NVFP4 && (!wamax || !xamax || !aligned(wamax, 4) || !aligned(xamax, 4)))
+    return fail(MX_E_INVALID, "gemm_blockscaled: NVFP4 needs both amax pointers");
   if (M < 0 || N < 0 || K <= 0 || K % 32 || ldy < N || !wq || !wsf || !xq || !xsf || !y || !aligned(wq, 16) ||
       !aligned(xq, 16) || !aligned(wsf, 4) || !aligned(xsf, 4) || !aligned(y, 2))
     return fail(MX_E_INVALID, "gemm_blockscaled: bad arguments (M=%lld N=%lld K=%lld)", (long long)M, (long long)N,
@@ -489,6 +503,12 @@ int mx_gemm_blockscaled(int mode, const void* wq, const void* wsf, const void* x
   if ((N + 255) / 256 * 256 * K >= (int64_t(1) << 31) || (M + 255) / 256 * 256 * K >= (int64_t(1) << 31) ||
       M > 0x7fffffff || N > 0x7fffffff)
     return fail(MX_E_UNSUPPORTED, "gemm_blockscaled: matrix too large for 32-bit offsets");
+  if (mode == MX_QMODE_NVFP4)
+    return hip_status(mxa::launch_nvfp4_gemm(static_cast<const uint8_t*>(wq), static_cast<const uint8_t*>(wsf), wamax,
+                                             static_cast<const uint8_t*>(xq), static_cast<const uint8_t*>(xsf), xamax,
+                                             static_cast<uint16_t*>(y), ldy, int(M), int(N), int(K),
+                                             beta == 1.f ? 1 : 0, static_cast<hipStream_t>(stream)),
+                      "gemm_blockscaled");
   return hip_status(mxa::launch_mxfp8_gemm(static_cast<const uint8_t*>(wq), static_cast<const uint8_t*>(wsf),
                                            static_cast<const uint8_t*>(xq), static_cast<const uint8_t*>(xsf),
                                            static_cast<uint16_t*>(y), ldy, int(M), int(N), int(K), beta == 1.f ? 1 : 0,

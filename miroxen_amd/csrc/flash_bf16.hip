@@ -430,22 +430,6 @@ __device__ __forceinline__ void store_partial(const QBlock<DH>& X, const BfSplit
 // waited for before its MFMA; config-2 shape 176 -> 146 us with the target stated).
 // The non-causal kernels keep the equivalent of __launch_bounds__(512, 1): the stated
 // target changes their schedule for the worse at D = 64 and not at all at D = 128.
-#ifdef MX_STAMPS
-// Timing probe (debug builds only): per work-group, the 100 MHz chip clock at kernel
-// entry, after the prologue, after the tile loop and after the store, plus HW_ID and
-// XCC_ID.
-__device__ uint64_t g_stamps[1 << 20];
-__device__ __forceinline__ void stamp(int slot) {
-  if (threadIdx.x == 0) {
-    uint64_t* d = g_stamps + size_t(blockIdx.x) * 8;
-    d[slot] = __builtin_amdgcn_s_memrealtime();
-    if (slot == 0) d[6] = (uint64_t(__builtin_amdgcn_s_getreg(0xF814)) << 32) | __builtin_amdgcn_s_getreg(0xF804);
-  }
-}
-#define MX_STAMP(i) stamp(i)
-#else
-#define MX_STAMP(i)
-#endif
 
 template <int DH, bool CAUSAL, bool SPLIT>
 __global__ void __attribute__((amdgpu_flat_work_group_size(CAUSAL || DH == 128 ? 512 : 1, 512),

@@ -8,6 +8,7 @@
 //   ki [Hkv][skv_pad][D] int8  ks [Hkv][skv_pad/64] f32 (K: 64-token groups, mean removed)
 //   vt [Hkv][D][skv_pad] e4m3  va [Hkv][D] f32          (V^T, per-channel 448/amax)
 //   km [Hkv][D] f32 (K mean)   part [2][Hkv][nb][D] f32 (kv_stats partials, nb = ceil(Skv/256))
+#include <cstdlib>
 #include <type_traits>
 
 #include "attn_common.hpp"
@@ -823,6 +824,7 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
                uint16_t* o, mx_attn_params p, int64_t sq_pad, int64_t skv_pad, SageSplit sp,
                const uint16_t* qb, float qmult) {
   constexpr int NW = kPipeWaves, QT = NW * 32, D = kPipeD;
+  MX_STAMP(0);
   __shared__ __align__(16) unsigned char kring[4 * KTILEB];
   __shared__ __align__(16) unsigned char vring[4 * VTILEB];
   __shared__ __align__(16) u32x4 table[kPipeMaxTiles + 1];
@@ -943,6 +945,7 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   }
   wait_vm_n<0>();
   __syncthreads();  // K(tb..tb+3), V(tb), V(tb+1) and the tile table are visible
+  MX_STAMP(1);
 
   // per-lane LDS read bases
   const int krow = kperm(0, n);
@@ -1048,9 +1051,16 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
                : "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", "v211",
                  "v212", "v213", "v214", "v215", "v224", "v227", "v238", "vcc", "scc", "memory");
   wait_vm_n<0>();  // no LDS-DMA may land after the work-group ends
+  MX_STAMP(2);
   f32x16 acc[4] = {acc0, acc1, acc2, acc3};
   l += other_half(l);  // the wave halves summed different keys of the same rows
   sage_finish<NW, D>(acc, m, l, part, su, sp, wave, lane, row, p, vas, head, o);
+#ifdef MX_STAMPS
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  MX_STAMP(3);
+  if (threadIdx.x == 0) g_stamps[size_t(blockIdx.x) * 8 + 5] = uint64_t(part + 1);
+#endif
 }
 
 }  // namespace
@@ -1100,6 +1110,13 @@ SagePlan sage_plan(const mx_attn_params& p) {
     if (cost < best - 1e-9) best = cost, pl.parts = S;
   }
   if (pl.parts > 1) pl.full = U - r, pl.units = r;
+#ifdef MX_STAMPS
+  if (const char* e = getenv("MX_SAGE_PARTS")) {  // debug builds: force the part count
+    const int S = atoi(e);
+    pl = SagePlan{U, 0, 1};
+    if (S > 1) pl = SagePlan{U - r, r, S};
+  }
+#endif
   return pl;
 }
 
@@ -1246,3 +1263,9 @@ hipError_t launch_sage_fp8(const uint16_t* q, const uint16_t* k, const uint16_t*
 }
 
 }  // namespace mxa
+
+#ifdef MX_STAMPS
+extern "C" int mx_debug_stamps_sage(void* dst, size_t bytes) {
+  return int(hipMemcpyFromSymbol(dst, HIP_SYMBOL(mxa::g_stamps), bytes, 0, hipMemcpyDeviceToHost));
+}
+#endif

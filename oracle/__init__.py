@@ -67,6 +67,14 @@ def lib():
         L.or_mxfp8_quantize.argtypes = [_p, _i64, _i64, _i64, _p, _p]
         L.or_gemm_mxfp8.restype = None
         L.or_gemm_mxfp8.argtypes = [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i]
+        L.or_e2m1.restype = ctypes.c_uint8
+        L.or_e2m1.argtypes = [_f]
+        L.or_e2m1_to_f32.restype = _f
+        L.or_e2m1_to_f32.argtypes = [ctypes.c_uint8]
+        L.or_nvfp4_quantize.restype = None
+        L.or_nvfp4_quantize.argtypes = [_p, _i64, _i64, _i64, _p, _p, _p]
+        L.or_gemm_nvfp4.restype = None
+        L.or_gemm_nvfp4.argtypes = [_p, _p, _f, _p, _p, _f, _i64, _i64, _i64, _p, _i]
         L.or_num_threads.restype = _i
         _lib = L
     return _lib
@@ -193,6 +201,36 @@ def sage_reference(q, k, v, Sq, Skv, Hq, Hkv, D, scale=0.0, q_stride=0, kv_strid
     return out, dict(qi=qi, qs=qs, ki=ki, ks=ks, vt=vt, km=km, va=va)
 
 
+def e2m1(x: float) -> int:
+    return int(lib().or_e2m1(float(x)))
+
+
+def e2m1_to_f32(c: int) -> float:
+    return float(lib().or_e2m1_to_f32(int(c)))
+
+
+def nvfp4_quantize(x, rows, K, ldx=0):
+    """NVFP4 quantizer (reference blockscale.cu:45-93, :113-131): x bf16 bits [rows, ldx]
+    -> (q uint8 [rows, K/2] two e2m1 codes per byte, low nibble first; sf uint8
+    [rows, K/16] e4m3, logical order; amax float)."""
+    x = _c(x, np.uint16)
+    ldx = ldx or K
+    q = np.zeros((rows, K // 2), np.uint8)
+    sf = np.zeros((rows, K // 16), np.uint8)
+    amax = np.zeros(1, np.float32)
+    lib().or_nvfp4_quantize(_ptr(x), ldx, rows, K, _ptr(q), _ptr(sf), _ptr(amax))
+    return q, sf, float(amax[0])
+
+
+def gemm_nvfp4(wq, wsf, wamax, xq, xsf, xamax, M, N, K, threads=0):
+    """Y[M, N] = alpha deq(X) deq(W)^T (sum in float64, alpha = gW gX in float)."""
+    wq = _c(wq, np.uint8); wsf = _c(wsf, np.uint8); xq = _c(xq, np.uint8); xsf = _c(xsf, np.uint8)
+    out = np.zeros((M, N), np.float32)
+    lib().or_gemm_nvfp4(_ptr(wq), _ptr(wsf), float(wamax), _ptr(xq), _ptr(xsf), float(xamax), M, N, K, _ptr(out),
+                        threads)
+    return out
+
+
 def num_threads() -> int:
     return int(lib().or_num_threads())
 
@@ -231,10 +269,10 @@ def mx_sf_offset(r, kb, nkb_pad):
     return (r // 128) * nkb_pad * 128 + (kb // 4) * 512 + (r % 32) * 16 + (r % 128) // 32 * 4 + kb % 4
 
 
-def mx_scale_pack(sf, rows, K, fill=127):
-    """Logical scales [rows, K/32] -> the interleaved buffer (pad128(rows) x pad4(K/32) bytes);
-    padding positions hold `fill`."""
-    nkb = K // 32
+def mx_scale_pack(sf, rows, K, fill=127, vec=32):
+    """Logical scales [rows, K/vec] -> the interleaved buffer (pad128(rows) x pad4(K/vec)
+    bytes; vec 32 for MXFP8, 16 for NVFP4); padding positions hold `fill`."""
+    nkb = K // vec
     nkp = (nkb + 3) // 4 * 4
     buf = np.full(((rows + 127) // 128 * 128) * nkp, fill, np.uint8)
     r, kb = np.meshgrid(np.arange(rows), np.arange(nkb), indexing="ij")
@@ -242,9 +280,9 @@ def mx_scale_pack(sf, rows, K, fill=127):
     return buf
 
 
-def mx_scale_unpack(buf, rows, K):
-    """The interleaved scale buffer -> logical scales [rows, K/32]."""
-    nkb = K // 32
+def mx_scale_unpack(buf, rows, K, vec=32):
+    """The interleaved scale buffer -> logical scales [rows, K/vec]."""
+    nkb = K // vec
     nkp = (nkb + 3) // 4 * 4
     r, kb = np.meshgrid(np.arange(rows), np.arange(nkb), indexing="ij")
     return np.asarray(buf, np.uint8).reshape(-1)[mx_sf_offset(r, kb, nkp)]

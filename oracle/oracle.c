@@ -40,6 +40,14 @@
  *    reference decoder's formula and the bijection onto the padded buffer.
  *  - or_gemm_mxfp8: pinned by a numpy float64 dequantize-and-matmul and the
  *    identity-weight case (W = I with unit scales returns deq(X)).
+ *  - or_e2m1: pinned by a nearest-value search over the e2m1 grid with ties to the
+ *    even code (all midpoints), saturation and signs.
+ *  - or_nvfp4_quantize: pinned by numpy's max |x| for amax, hand cases (the tensor's
+ *    largest element gets scale 448 and code 6, a zero block scale 0 and codes 0,
+ *    amax = 0 gives g = 1), the scale against e4m3 of float64 bmax / (6 g) and the
+ *    element error bound (half an e2m1 step of the block, or saturation at 6).
+ *  - or_gemm_nvfp4: pinned by a numpy float64 decode (the reference test's decoder,
+ *    tests/blockscale_test.cpp:37-43) and matmul times alpha.
  */
 #include <math.h>
 #include <stdint.h>
@@ -554,6 +562,92 @@ void or_gemm_mxfp8(const uint8_t* wq, const uint8_t* wsf, const uint8_t* xq, con
         acc += blk * ldexp(1.0, (int)xsf[m * nkb + kb] - 127) * ldexp(1.0, (int)wsf[n * nkb + kb] - 127);
       }
       out[m * N + n] = (float)acc;
+    }
+}
+
+/* ---------- NVFP4 (reference src/kernels/blockscale.cu, NVFP4 branch) ----------
+ * e2m1 (OCP FP4: 1 sign, 2 exponent, 1 mantissa bit; magnitudes 0, 0.5, 1, 1.5, 2, 3,
+ * 4, 6) of x, rounded to the nearest magnitude with ties to the even code and
+ * saturated to 6, as the reference's threshold sum (blockscale.cu:38-42): a
+ * magnitude code counts the thresholds 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5 that |x|
+ * passes, strictly above the ones whose lower neighbour has an even code (0.25,
+ * 1.25, 2.5, 5) and at or above the others. Sign bit 8 for x < 0 (so -0 and NaN
+ * encode with sign 0). */
+uint8_t or_e2m1(float x) {
+  const float a = fabsf(x);
+  const uint8_t c = (uint8_t)((a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) +
+                              (a > 5.f));
+  return (uint8_t)(c | (x < 0.f ? 8 : 0));
+}
+
+float or_e2m1_to_f32(uint8_t c) {
+  static const float mag[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+  const float v = mag[c & 7];
+  return (c & 8) ? -v : v;
+}
+
+/* quantize_blockscaled(NVFP4) (blockscale.cu:113-131 with amax_kernel :45-67 and
+ * quant_kernel's NVFP4 branch :69-93): amax = max |x| over the tensor; g = amax / (6 *
+ * 448) (1 when amax = 0); per 16-value block se = e4m3(bmax / (6 g)) (saturating, round
+ * to nearest even), sd = float(se) g, inv = 1 / sd (0 when sd = 0), code j = e2m1(x_j
+ * inv); two codes per byte, the lower-index value in the low nibble. sf: logical
+ * [rows][K/16] e4m3 bytes. Float arithmetic in the reference's order. */
+void or_nvfp4_quantize(const uint16_t* x, int64_t ldx, int64_t rows, int64_t K, uint8_t* q, uint8_t* sf,
+                       float* amax_out) {
+  float amax = 0.f;
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t k = 0; k < K; ++k) {
+      const float a = fabsf(or_bf16_to_f32(x[r * ldx + k]));
+      if (a > amax) amax = a;
+    }
+  *amax_out = amax;
+  const float g = amax > 0.f ? amax / (6.f * 448.f) : 1.f;
+  const float inv6g = 1.f / (6.f * g);
+  const int64_t nkb = K / 16;
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t kb = 0; kb < nkb; ++kb) {
+      float v[16], bmax = 0.f;
+      for (int j = 0; j < 16; ++j) {
+        v[j] = or_bf16_to_f32(x[r * ldx + kb * 16 + j]);
+        if (fabsf(v[j]) > bmax) bmax = fabsf(v[j]);
+      }
+      const uint8_t se = or_e4m3(bmax * inv6g);
+      const float sd = or_e4m3_to_f32(se) * g;
+      const float inv = sd > 0.f ? 1.f / sd : 0.f;
+      uint8_t* dst = q + (r * K + kb * 16) / 2;
+      for (int j = 0; j < 8; ++j)
+        dst[j] = (uint8_t)(or_e2m1(v[2 * j] * inv) | (or_e2m1(v[2 * j + 1] * inv) << 4));
+      sf[r * nkb + kb] = se;
+    }
+}
+
+/* gemm_blockscaled(NVFP4) (blockscale.cu:134-216: cuBLASLt with VEC16_UE4M3 block
+ * scales and alpha = gW gX from alpha_kernel :111-115): Y[m][n] = alpha * sum_k
+ * (e2m1 x se)_X (e2m1 x se)_W, the sum in double, alpha in float as the reference
+ * computes it. sf [rows][K/16] logical order. out [M][N] float. */
+void or_gemm_nvfp4(const uint8_t* wq, const uint8_t* wsf, float wamax, const uint8_t* xq, const uint8_t* xsf,
+                   float xamax, int64_t M, int64_t N, int64_t K, float* out, int threads) {
+  const int64_t nkb = K / 16;
+  const float gw = wamax > 0.f ? wamax / (6.f * 448.f) : 1.f, gx = xamax > 0.f ? xamax / (6.f * 448.f) : 1.f;
+  const float alpha = gw * gx;
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) {
+      double acc = 0.0;
+      for (int64_t kb = 0; kb < nkb; ++kb) {
+        double blk = 0.0;
+        for (int j = 0; j < 16; ++j) {
+          const int64_t k = kb * 16 + j;
+          const uint8_t cx = (uint8_t)((xq[(m * K + k) / 2] >> ((k & 1) * 4)) & 15);
+          const uint8_t cw = (uint8_t)((wq[(n * K + k) / 2] >> ((k & 1) * 4)) & 15);
+          blk += (double)or_e2m1_to_f32(cx) * (double)or_e2m1_to_f32(cw);
+        }
+        acc += blk * (double)or_e4m3_to_f32(xsf[m * nkb + kb]) * (double)or_e4m3_to_f32(wsf[n * nkb + kb]);
+      }
+      out[m * N + n] = (float)(acc * (double)alpha);
     }
 }
 

@@ -624,3 +624,91 @@ def test_mxfp8_gemm_oracle_matches_numpy():
     ones = np.full((K, K // 32), 127, np.uint8)
     got = oracle.gemm_mxfp8(eye, ones, xq, xs, M, K, K)
     np.testing.assert_array_equal(got, dq(xq, xs).astype(np.float32))
+
+
+# ---------------- NVFP4 (reference src/kernels/blockscale.cu, NVFP4 branch) ----------------
+
+_E2M1 = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6], np.float64)
+
+
+def _e2m1_decode(codes):
+    """The reference test's decoder (tests/blockscale_test.cpp:37-43): sign bit 8,
+    magnitude table {0, 0.5, 1, 1.5, 2, 3, 4, 6}."""
+    codes = np.asarray(codes)
+    return np.where(codes & 8, -1.0, 1.0) * _E2M1[codes & 7]
+
+
+def test_e2m1_is_nearest_even_by_search():
+    """Every midpoint and random values: the code of the nearest e2m1 magnitude, ties to
+    the even code, saturating at 6; the sign bit for negative values."""
+    mids = (_E2M1[:-1] + _E2M1[1:]) / 2
+    rng = np.random.default_rng(41)
+    xs = np.concatenate([mids, -mids, _E2M1, -_E2M1[1:], rng.uniform(-8, 8, 2000), [6.5, 100.0, -1e9]])
+    for x in xs.astype(np.float32):
+        a = abs(float(x))
+        d = np.abs(_E2M1 - min(a, 6.0))
+        best = np.flatnonzero(d == d.min())
+        code = int(best[0]) if len(best) == 1 else int([b for b in best if b % 2 == 0][0])
+        want = code | (8 if x < 0 else 0)
+        assert oracle.e2m1(x) == want, (x, oracle.e2m1(x), want)
+        assert oracle.e2m1_to_f32(want) == _e2m1_decode(want)
+
+
+def test_nvfp4_quantizer_rules():
+    """amax = max |x| (numpy); the tensor's largest element gets scale 448 and code 6; a
+    zero block gets scale 0 and codes 0; every block scale is the e4m3 of float64
+    bmax / (6 g) up to the float rounding of the reference's single-precision steps (one
+    e4m3 step at most, only where float64 lands within 1e-6 of a rounding boundary);
+    elements decode to within half an e2m1 step of x / sd, or saturate at 6."""
+    rng = np.random.default_rng(42)
+    rows, K = 5, 160
+    x = (rng.standard_normal((rows, K)) * np.exp2(rng.integers(-6, 6, (rows, 1)))).astype(np.float32)
+    x[0, :16] = 0.0
+    x[3, 37] = 1000.0
+    xb = oracle.f32_to_bf16(x)
+    q, sf, amax = oracle.nvfp4_quantize(xb, rows, K)
+    xf = oracle.bf16_to_f32(xb).astype(np.float64)
+    assert amax == np.abs(xf).max() == 1000.0
+    g = amax / (6 * 448)
+    codes = np.stack([q & 15, q >> 4], -1).reshape(rows, K)
+    t = _e4m3_lut()
+    assert sf[3, 37 // 16] == 0x7E and codes[3, 37] == 7        # 448 and +6
+    assert sf[0, 0] == 0 and np.all(codes[0, :16] == 0)
+    bmax = np.abs(xf.reshape(rows, K // 16, 16)).max(-1)
+    near = np.array([[oracle.e4m3(np.float32(b / (6 * g))) for b in row] for row in bmax])
+    assert np.all(np.abs(sf.astype(np.int64) - near.astype(np.int64)) <= 1)
+    sd = t[sf] * g
+    y = xf.reshape(rows, K // 16, 16) / np.where(sd > 0, sd, 1)[..., None]
+    dec = _e2m1_decode(codes).reshape(rows, K // 16, 16)
+    step = np.where(np.abs(y) < 2, 0.5, np.where(np.abs(y) < 4, 1.0, 2.0))
+    ok = (np.abs(dec - y) <= step / 2 * (1 + 1e-6)) | ((np.abs(dec) == 6) & (np.abs(y) >= 5))
+    assert np.all(ok | (sd[..., None] == 0))
+    # amax = 0: g = 1, every scale and code 0
+    q0, sf0, a0 = oracle.nvfp4_quantize(np.zeros((2, 32), np.uint16), 2, 32)
+    assert a0 == 0.0 and not q0.any() and not sf0.any()
+
+
+def test_nvfp4_gemm_oracle_matches_numpy():
+    """The GEMM oracle against a numpy float64 decode (the reference test's decoder) and
+    matmul, scaled by alpha = gW gX."""
+    rng = np.random.default_rng(43)
+    M, N, K = 6, 5, 96
+    xb = oracle.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32) * 3)
+    wb = oracle.f32_to_bf16(rng.standard_normal((N, K)).astype(np.float32) * 0.02)
+    xq, xs, xa = oracle.nvfp4_quantize(xb, M, K)
+    wq, ws, wa = oracle.nvfp4_quantize(wb, N, K)
+    t = _e4m3_lut()
+
+    def dq(q, s, amax):
+        codes = np.stack([q & 15, q >> 4], -1).reshape(q.shape[0], -1)
+        g = np.float32(amax) / np.float32(6 * 448)
+        return (_e2m1_decode(codes).reshape(q.shape[0], -1, 16) * t[s][..., None]).reshape(codes.shape), g
+
+    dx, gx = dq(xq, xs, xa)
+    dw, gw = dq(wq, ws, wa)
+    want = (dx @ dw.T) * float(np.float32(gx * gw))
+    got = oracle.gemm_nvfp4(wq, ws, wa, xq, xs, xa, M, N, K)
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-12)
+    # and the decoded product approximates the bf16 GEMM (the reference's gate: 15 %)
+    ref = oracle.bf16_to_f32(xb).astype(np.float64) @ oracle.bf16_to_f32(wb).astype(np.float64).T
+    assert np.sqrt(((got - ref) ** 2).sum() / (ref ** 2).sum()) < 0.15
