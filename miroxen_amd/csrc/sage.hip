@@ -540,7 +540,8 @@ __device__ __forceinline__ void sage_load_tile(const SageAddr<D>& a, int tk, int
 template <int NW, int D>
 __device__ __forceinline__ void sage_finish(f32x16 (&acc)[D / 32], float m, float l, int part, int su, const SageSplit& sp,
                                             int wave, int lane, int row, const mx_attn_params& p,
-                                            const float* __restrict__ vah, int head, uint16_t* __restrict__ o) {
+                                            const float* __restrict__ vah, int head, uint16_t* __restrict__ o,
+                                            unsigned char* stage = nullptr) {
   const int h = lane >> 5;
   if (part >= 0) {
     // Split unit: publish (o, m, l), then the last part to arrive merges all parts.
@@ -624,6 +625,37 @@ __device__ __forceinline__ void sage_finish(f32x16 (&acc)[D / 32], float m, floa
     }
   }
   // ---- epilogue: O = acc * vamax[d] / (448 l) -> bf16 ----
+  // Through LDS when the caller lends a staging buffer (NW * 32 rows x D bf16) and the
+  // output allows 16-byte row stores: each wave writes its 32 x D block into its region
+  // (16-byte chunks of row n XOR-swizzled by n), then every lane stores 16 contiguous
+  // bytes, 1 KB of whole rows per instruction instead of 4-byte pieces of 32 rows.
+  if (stage && (reinterpret_cast<uintptr_t>(o) & 15) == 0 && (p.o_stride & 7) == 0) {
+    constexpr int CH = D / 8, RB = D * 2;
+    const int n = lane & 31;
+    const float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
+    MXA_LDS unsigned char* wb = (MXA_LDS unsigned char*)stage + wave * 32 * RB;
+    __syncthreads();  // every wave is done with the buffer (the tile loop's K ring)
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + g * 8 + h * 4;
+        const f32x4 sv = *reinterpret_cast<const f32x4*>(vah + d);
+        const int phys = (db * 4 + g) ^ (n & (CH - 1));
+        *reinterpret_cast<MXA_LDS u32x2*>(wb + n * RB + phys * 16 + h * 8) =
+            u32x2{pack_bf16x2(acc[db][g * 4] * sv[0] * inv, acc[db][g * 4 + 1] * sv[1] * inv),
+                  pack_bf16x2(acc[db][g * 4 + 2] * sv[2] * inv, acc[db][g * 4 + 3] * sv[3] * inv)};
+      }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const int row0 = row - n;
+#pragma unroll
+    for (int i = 0; i < 32 * CH / 64; ++i) {
+      const int idx = i * 64 + lane, r = idx / CH, c = idx % CH;
+      const u32x4 val = *reinterpret_cast<const MXA_LDS u32x4*>(wb + r * RB + ((c ^ (r & (CH - 1))) * 16));
+      if (row0 + r < p.Sq) *reinterpret_cast<u32x4*>(o + int64_t(row0 + r) * p.o_stride + head * D + c * 8) = val;
+    }
+    return;
+  }
   if (row < p.Sq) {
     const float inv = l > 0.f ? 1.f / (448.f * l) : 0.f;
     uint16_t* dst = o + int64_t(row) * p.o_stride + head * D + h * 4;
@@ -1054,7 +1086,7 @@ sage_attn_pipe(const int8_t* __restrict__ qi, const int8_t* __restrict__ ki, con
   MX_STAMP(2);
   f32x16 acc[4] = {acc0, acc1, acc2, acc3};
   l += other_half(l);  // the wave halves summed different keys of the same rows
-  sage_finish<NW, D>(acc, m, l, part, su, sp, wave, lane, row, p, vas, head, o);
+  sage_finish<NW, D>(acc, m, l, part, su, sp, wave, lane, row, p, vas, head, o, kring);
 #ifdef MX_STAMPS
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
