@@ -172,6 +172,36 @@ def test_mask_equals_compacted_keys(cuda):
     assert cosine(_f32(o1), _f32(o2)) > 0.99999
 
 
+@pytest.mark.parametrize("Skv", [20000, 3000])
+def test_mask_bitmap_paths(cuda, Skv):
+    """The key-padding bitmaps are built from 16-byte loads when the mask is 16-byte
+    aligned (two 1024-key chunks per wave up front, the rest after: Skv = 20000 needs 20
+    chunks) and from byte loads otherwise: a random mask at an aligned and at an odd
+    address gives bit-identical outputs, both against the oracle on sampled rows."""
+    Sq, H, D = 256, 2, 128
+    print(f"mask bitmaps Skv={Skv}", flush=True)
+    q, k, v, *_ = _make(Sq, Skv, H, H, D, 0, 1.0, Skv, cuda)
+    g = torch.Generator().manual_seed(Skv)
+    mask = (torch.rand(Skv, generator=g) > 0.35).to(torch.uint8)
+    mask[Skv - 70:] = 0  # a dead tail spanning a tile boundary
+    base = torch.zeros(Skv + 64, dtype=torch.uint8, device=cuda)
+    aligned, odd = base[:Skv], base[17:17 + Skv]
+    aligned.copy_(mask.to(cuda))
+    o1 = torch.empty_like(q)
+    flash_attn(q, k, v, o1, AttnParams(Sq=Sq, Skv=Skv, Hq=H, Hkv=H, D=D, kv_valid=aligned))
+    torch.cuda.synchronize()
+    odd.copy_(mask.to(cuda))
+    o2 = torch.empty_like(q)
+    flash_attn(q, k, v, o2, AttnParams(Sq=Sq, Skv=Skv, Hq=H, Hkv=H, D=D, kv_valid=odd))
+    torch.cuda.synchronize()
+    assert odd.data_ptr() % 16 != 0 and aligned.data_ptr() % 16 == 0
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    rows = np.array([0, 1, 100, 255], np.int32)
+    want = oracle.attention_f64(_bits(q), _bits(k), _bits(v), Sq, Skv, H, H, D, kv_valid=mask.numpy(), rows=rows)
+    got = _f32(o1)[rows].reshape(want.shape)
+    assert cosine(got, want) >= 0.9999 and max_abs(got, want) <= 2e-2
+
+
 def test_all_masked_and_deterministic(cuda):
     S, H = 300, 2
     q, k, v, *_ = _make(S, S, H, H, 128, 0, 1.0, 5, cuda)
