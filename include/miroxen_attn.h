@@ -138,6 +138,8 @@ typedef struct mx_sage_layout {
   int split_qt; /* query rows per grid unit of the attention kernel (128 or 256) */
   size_t tab;   /* [Hkv][skv_pad/64 + 1] 16-byte tile entries: liveness bits, K scale (negated
                    when some key of the tile is dead) */
+  size_t flg;   /* [Hkv][nb] 64-bit ready flags of the one-pass K/V prologue, one per
+                   256-token statistics block (nb = ceil(Skv/256)) */
 } mx_sage_layout;
 int mx_sage_layout_of(const mx_attn_params* p, mx_sage_layout* out);
 
@@ -152,6 +154,13 @@ int mx_sage_quantize(const void* q, const void* k, const void* v, const mx_attn_
  * of its four 16-token entries), so mx_sage_attend runs on it as it is. */
 int mx_sage_quantize_qgroup(const void* q, const void* k, const void* v, const mx_attn_params* p, void* ws,
                             int q_group, void* stream);
+
+/* Test hook, no reference counterpart: the bound, in ticks of the 100 MHz chip clock
+ * (default 20000 = 200 us), on how long a work-group of the one-pass K/V prologue waits
+ * for the other statistics blocks of its head before it computes their partials from K
+ * and V itself (same bytes, so the workspace does not change). 0 = one look. Process-wide;
+ * for tests of that recompute path. */
+int mx_sage_prologue_wait_ticks(int64_t ticks);
 
 /* Main kernel only, on a workspace already filled by mx_sage_quantize (or
  * mx_sage_quantize_qgroup / mx_sage_quantize_norm_rope). A workspace last used by

@@ -20,7 +20,7 @@ SYMBOLS = (
     "mx_flash_attn_fp8_noalloc",
     "mx_attn_reference", "mx_sage_layout_of",
     "mx_sage_quantize", "mx_sage_attend", "mx_last_error", "mx_version", "mx_head_norm_rope",
-    "mx_sage_quantize_norm_rope", "mx_flash_attn_fp8_norm_rope", "mx_sage_quantize_qgroup",
+    "mx_sage_quantize_norm_rope", "mx_flash_attn_fp8_norm_rope", "mx_sage_quantize_qgroup", "mx_sage_prologue_wait_ticks",
     "mx_qmode_supported", "mx_qdata_bytes", "mx_qscale_bytes", "mx_quantize_blockscaled", "mx_gemm_blockscaled",
 )
 
@@ -45,7 +45,7 @@ class CLayout(ctypes.Structure):
     _fields_ = [("sq_pad", ctypes.c_int64), ("skv_pad", ctypes.c_int64)] + [
         (n, ctypes.c_size_t) for n in ("qi", "ki", "vt", "qs", "ks", "km", "va", "part", "split", "cnt", "total")] + [
         ("split_units", ctypes.c_int), ("split_parts", ctypes.c_int), ("split_qt", ctypes.c_int),
-        ("tab", ctypes.c_size_t)]
+        ("tab", ctypes.c_size_t), ("flg", ctypes.c_size_t)]
 
 
 _lib = None
@@ -73,6 +73,7 @@ def load():
         "mx_sage_layout_of": ([P, ctypes.POINTER(CLayout)], ctypes.c_int),
         "mx_sage_quantize": ([vp, vp, vp, P, vp, vp], ctypes.c_int),
         "mx_sage_quantize_qgroup": ([vp, vp, vp, P, vp, ctypes.c_int, vp], ctypes.c_int),
+        "mx_sage_prologue_wait_ticks": ([ctypes.c_int64], ctypes.c_int),
         "mx_sage_attend": ([vp, P, vp, vp], ctypes.c_int),
         "mx_last_error": ([], ctypes.c_char_p),
         "mx_version": ([], ctypes.c_char_p),

@@ -26,6 +26,7 @@ mx_sage_layout sage_layout(const mx_attn_params&);
 hipError_t launch_sage_quantize(const uint16_t*, const uint16_t*, const uint16_t*, const mx_attn_params&, char*,
                                 hipStream_t, const NormRope*, int q_group);
 hipError_t launch_sage_attend(uint16_t*, const mx_attn_params&, const char*, hipStream_t);
+void set_prologue_wait_ticks(uint64_t);
 hipError_t launch_sage_fp8(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, const mx_attn_params&, char*,
                            hipStream_t);
 size_t mx_qscale_size(int64_t rows, int64_t K);
@@ -332,6 +333,12 @@ int mx_sage_quantize(const void* q, const void* k, const void* v, const mx_attn_
                                               static_cast<const uint16_t*>(v), a, static_cast<char*>(ws),
                                               static_cast<hipStream_t>(stream), nullptr, 16),
                     "sage_quantize");
+}
+
+int mx_sage_prologue_wait_ticks(int64_t ticks) {
+  if (ticks < 0) return fail(MX_E_INVALID, "sage_prologue_wait_ticks: negative bound");
+  mxa::set_prologue_wait_ticks(uint64_t(ticks));
+  return MX_OK;
 }
 
 int mx_sage_quantize_qgroup(const void* q, const void* k, const void* v, const mx_attn_params* p, void* ws,

@@ -8,7 +8,10 @@
 //   ki [Hkv][skv_pad][D] int8  ks [Hkv][skv_pad/64] f32 (K: 64-token groups, mean removed)
 //   vt [Hkv][D][skv_pad] e4m3  va [Hkv][D] f32          (V^T, per-channel 448/amax)
 //   km [Hkv][D] f32 (K mean)   part [2][Hkv][nb][D] f32 (kv_stats partials, nb = ceil(Skv/256))
+#include <atomic>
+#include <chrono>
 #include <cstdlib>
+#include <random>
 #include <type_traits>
 
 #include "attn_common.hpp"
@@ -372,6 +375,350 @@ __global__ void __launch_bounds__(256) prep_kv_quant(const uint16_t* __restrict_
     *reinterpret_cast<u32x4*>(vt + (int64_t(h) * D + d) * skv_pad + k0 + u * 16) =
         *reinterpret_cast<const u32x4*>(&tile[d][16 * (u ^ ((d >> 4) & 3))]);
   }
+}
+
+// ---------------- one-pass K/V prologue ----------------
+//
+// prep_kv_fused replaces prep_stats_q's K/V blocks, prep_finalize and prep_kv_quant
+// with one launch that reads K and V once: work-group (h, b) loads its 256-token
+// block of K and V into registers, publishes the block's statistics partial
+// (sequential K sum / Skv, V abs-max) and a ready flag, waits until its head's
+// K mean and V abs-max are known, and quantizes the block from its registers.
+// Same arithmetic as the three-launch path (bit-identical workspace).
+//
+// Flags: ws.flg holds one 64-bit word per (head, block); a word is
+// "set" when it equals the call's epoch, a per-process counter that never repeats
+// (and is never 0), so no flag needs clearing before a call and a workspace reused
+// across calls cannot satisfy a wait with an old flag. The host runs this path only
+// outside stream capture: a captured launch would replay with one fixed epoch.
+//
+// Waiting: work-groups are dispatched in index order and a head's blocks are
+// consecutive, so a head's blocks all get a slot while earlier heads drain (a head
+// holds at most kFoldNb work-groups). The wait is bounded all the same: after
+// kFusedWaitTicks of the 100 MHz chip clock a work-group stops waiting and computes
+// every partial whose flag it has not seen from K and V in memory (the same bytes
+// the missing block would write), so the kernel ends whatever the dispatch order.
+//
+// Every work-group sums its head's nb <= kFoldNb partials itself. Beyond that (Skv >
+// 8192) the three-launch path runs: a variant in which the head's last block folded
+// the partials and published them with a head flag measured no faster at 49 blocks
+// per head and slower at 128 (its waiting work-groups hold slots the loads need).
+//
+// Memory ordering across work-groups (and XCDs, whose L2s are not coherent): partials
+// and flags move with device-scope relaxed atomics (sc1 accesses, served at the
+// device-coherent level); a publisher waits for its stores' acknowledgements
+// (vmcnt(0)) and passes a work-group barrier before lane 0 stores the flag, and a
+// reader loads the data only after the barrier that follows its flag loads.
+constexpr uint64_t kFusedWaitTicks = 20000;  // 200 us
+// Bound in use (mx_sage_prologue_wait_ticks changes it for tests of the recompute path).
+std::atomic<uint64_t> g_fused_wait_ticks{kFusedWaitTicks};
+
+__device__ __forceinline__ void st_dev(float* p, float x) {
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// True when flags f[0..n) all equal epoch; false once `ticks` of the chip clock have
+// passed (ticks 0: one look). Work-group uniform; every thread must call it.
+__device__ __forceinline__ bool wait_flags(const uint64_t* f, int n, uint64_t epoch, uint64_t ticks) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  for (;;) {
+    bool ok = true;
+    for (int j = threadIdx.x; j < n; j += blockDim.x)
+      ok &= __hip_atomic_load(const_cast<uint64_t*>(f + j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
+    if (__syncthreads_and(ok)) return true;
+    const bool late = threadIdx.x == 0 && __builtin_amdgcn_s_memrealtime() - t0 >= ticks;
+    if (__syncthreads_or(late)) return false;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// Statistics partial of block b of head h computed from K and V in memory (the
+// fallback of a wait that timed out), staged through `sm` in 128-token chunks exactly
+// as prep_stats_q does, stored with device-scope stores. Threads < D: K sum, D..2D-1:
+// V abs-max.
+template <int D>
+__device__ void fused_stats_from_memory(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                        const mx_attn_params& p, int h, int b, int nb, float* part,
+                                        unsigned char* sm) {
+  uint16_t* kt = reinterpret_cast<uint16_t*>(sm);
+  uint16_t* vt_ = kt + kStatChunk * D;
+  const int tid = threadIdx.x;
+  const int64_t t0 = int64_t(b) * kStatTok;
+  const int64_t t1 = t0 + kStatTok < p.Skv ? t0 + kStatTok : p.Skv;
+  float sum = 0.f, am = 0.f;
+  for (int64_t c0 = t0; c0 < t1; c0 += kStatChunk) {
+    const int rows = int(t1 - c0 < kStatChunk ? t1 - c0 : kStatChunk);
+    __syncthreads();
+    for (int i = tid; i < rows * (D / 8); i += blockDim.x) {
+      const int r = i / (D / 8), c = (i % (D / 8)) * 8;
+      const int64_t g = (c0 + r) * p.kv_stride + int64_t(h) * D + c;
+      *reinterpret_cast<u32x4*>(&kt[r * D + c]) = *reinterpret_cast<const u32x4*>(k + g);
+      *reinterpret_cast<u32x4*>(&vt_[r * D + c]) = *reinterpret_cast<const u32x4*>(v + g);
+    }
+    __syncthreads();
+    if (tid < D) {
+      for (int r = 0; r < rows; ++r) sum += bf2f(kt[r * D + tid]);
+    } else if (tid < 2 * D) {
+      for (int r = 0; r < rows; ++r) am = fmaxf(am, fabsf(bf2f(vt_[r * D + tid - D])));
+    }
+  }
+  if (tid < D) st_dev(part + (int64_t(h) * nb + b) * D + tid, sum / float(p.Skv));
+  else if (tid < 2 * D) st_dev(part + int64_t(p.Hkv) * nb * D + (int64_t(h) * nb + b) * D + (tid - D), am);
+  __syncthreads();
+}
+
+// Wait for every block flag of head h (bounded), compute the partials still missing,
+// and return this thread's channel of K mean / V abs-max (threads < D) summed in
+// ascending block order (finalize_channel's arithmetic on device-scope loads).
+template <int D>
+__device__ void fused_fold(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, const mx_attn_params& p,
+                           int h, int nb, float* part, const uint64_t* flg, uint64_t epoch, uint64_t ticks,
+                           unsigned char* sm, bool* miss, float& s, float& am) {
+  const uint64_t* fh = flg + int64_t(h) * nb;
+  if (!wait_flags(fh, nb, epoch, ticks)) {
+    for (int j = threadIdx.x; j < nb; j += blockDim.x)
+      miss[j] = __hip_atomic_load(const_cast<uint64_t*>(fh + j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch;
+    __syncthreads();
+    for (int j = 0; j < nb; ++j)
+      if (miss[j]) fused_stats_from_memory<D>(k, v, p, h, j, nb, part, sm);
+    wait_vm();
+    __syncthreads();
+  }
+  // the head's partials: 16-byte device-scope loads by every thread (all issued before
+  // the first is used), staged in LDS, then each channel summed in ascending block order
+  // (finalize_channel's arithmetic); at most kFoldNb blocks per pass
+  s = 0.f;
+  am = 0.f;
+  float* pl = reinterpret_cast<float*>(sm);  // [2][kFoldNb][D]
+  constexpr int kSc1 = 16;                    // cache policy: device scope
+  const int64_t half = int64_t(p.Hkv) * nb * D;
+  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(part + int64_t(h) * nb * D, uint32_t(nb) * D * 4u);
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(part + half + int64_t(h) * nb * D, uint32_t(nb) * D * 4u);
+  constexpr int NQ = 2 * kFoldNb * D / 4 / 512;  // 16-byte loads per thread per pass
+  for (int b0 = 0; b0 < nb; b0 += kFoldNb) {
+    const int nbp = nb - b0 < kFoldNb ? nb - b0 : kFoldNb;
+    u32x4 x[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int e = (int(threadIdx.x) + i * 512) * 4;  // float index in [2][kFoldNb][D]
+      const int which = e / (kFoldNb * D), r = e % (kFoldNb * D);
+      x[i] = u32x4{0, 0, 0, 0};
+      if (r < nbp * D)
+        x[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             which ? rv : rk, uint32_t(r) * 4u, uint32_t(b0) * D * 4u, kSc1));
+    }
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) *reinterpret_cast<u32x4*>(pl + (int(threadIdx.x) + i * 512) * 4) = x[i];
+    __syncthreads();
+    if (threadIdx.x < D)
+      for (int j = 0; j < nbp; ++j) {
+        s += pl[j * D + threadIdx.x];
+        am = fmaxf(am, pl[kFoldNb * D + j * D + threadIdx.x]);
+      }
+    __syncthreads();
+  }
+}
+
+// One work-group of 512 threads per (head, 256-token block): thread t owns channel
+// chunk c = t % (D/8) (8 channels) of the RPT consecutive tokens from (t / (D/8)) RPT.
+template <int D>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) prep_kv_fused(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                                     mx_attn_params p, int nb, int64_t skv_pad,
+                                                     float* __restrict__ part, float* __restrict__ km,
+                                                     float* __restrict__ va, int8_t* __restrict__ ki,
+                                                     float* __restrict__ ks, uint8_t* __restrict__ vt,
+                                                     u32x4* __restrict__ tab, int* __restrict__ cnt, int ncnt,
+                                                     uint64_t* __restrict__ flg, uint64_t epoch, uint64_t wait_ticks) {
+  static_assert(D == 64 || D == 128, "head dimension 64 or 128");
+  constexpr int NT = 512, CPR = D / 8, RPT = kStatTok * CPR / NT;  // chunks per row, tokens per thread
+  constexpr int TPT = kKvPad / RPT * CPR;                           // threads per 64-key tile (128)
+  constexpr int G = kStatTok / RPT, GSH = D == 128 ? 2 : 3;         // V^T granules per row, swizzle shift
+  static_assert(TPT == 128 && G / 8 == (1 << GSH), "layout");
+  __shared__ __align__(16) unsigned char sm[kStatTok * D * 2];  // K rows, then V^T
+  __shared__ float red[NT / 64][D];
+  __shared__ float kms[D], vas[D];
+  __shared__ bool miss[kFoldNb];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int h = blockIdx.x / nb, b = blockIdx.x % nb;
+  const int c = tid % CPR, r0 = (tid / CPR) * RPT;
+  const int64_t t0 = int64_t(b) * kStatTok;
+  const int rows = int(p.Skv - t0 < kStatTok ? p.Skv - t0 : kStatTok);
+  MX_STAMP(0);
+
+  u32x4 kr[RPT], vr[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    kr[i] = vr[i] = u32x4{0, 0, 0, 0};
+    if (r0 + i < rows) {
+      const int64_t g = (t0 + r0 + i) * p.kv_stride + int64_t(h) * D + c * 8;
+      kr[i] = *reinterpret_cast<const u32x4*>(k + g);
+      vr[i] = *reinterpret_cast<const u32x4*>(v + g);
+    }
+  }
+  if (blockIdx.x == 0)  // arrival counters of the attention kernel's split units start at zero
+    for (int i = tid; i < ncnt; i += NT) cnt[i] = 0;
+
+  // ---- statistics partial: K rows through LDS for the sequential per-channel sum,
+  // V abs-max from registers (a max does not depend on order) ----
+  // D = 128: channel-major [D][256 tokens] (16-byte chunk u of channel row d at chunk
+  // u ^ ((d ^ (d >> 3)) & 15): conflict-free both for the writes, 16 channels of one
+  // chunk per pass, and for the sum's reads, 16 channels' same chunk), so the sum reads
+  // 8 tokens per LDS read; D = 64: token-major [256][D]
+  uint16_t* kst = reinterpret_cast<uint16_t*>(sm);
+  if constexpr (D == 128) {
+#pragma unroll
+    for (int j2 = 0; j2 < 4; ++j2)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {
+        const int d = c * 8 + j2 * 2 + hi;
+        const uint32_t sel = hi ? 0x07060302u : 0x05040100u;  // high / low bf16 of each word
+        u32x4 col;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) col[m] = __builtin_amdgcn_perm(kr[2 * m + 1][j2], kr[2 * m][j2], sel);
+        *reinterpret_cast<u32x4*>(sm + d * 512 + ((r0 / 8) ^ ((d ^ (d >> 3)) & 15)) * 16) = col;
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) *reinterpret_cast<u32x4*>(&kst[(r0 + i) * D + c * 8]) = kr[i];
+  }
+  // |v| as bf16 bits (sign cleared) ordered as integers: a packed 16-bit max per pair
+  // of channels equals the float max of |v| for every non-NaN input
+  using u16x2 = __attribute__((ext_vector_type(2))) unsigned short;
+  u16x2 vam[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    vam[w] = u16x2{0, 0};
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      vam[w] = __builtin_elementwise_max(vam[w], __builtin_bit_cast(u16x2, uint32_t(vr[i][w] & 0x7fff7fffu)));
+#pragma unroll
+    for (int off = CPR; off < 64; off <<= 1)
+      vam[w] = __builtin_elementwise_max(
+          vam[w], __builtin_bit_cast(u16x2, uint32_t(__shfl_xor(int(__builtin_bit_cast(uint32_t, vam[w])), off))));
+  }
+  if (lane < CPR)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) red[wave][c * 8 + j] = bf2f(vam[j >> 1][j & 1]);
+  __syncthreads();
+  MX_STAMP(1);
+  if (tid < D) {
+    float sum = 0.f;
+    if constexpr (D == 128) {  // tokens past the block's end are zeros: adding +0 changes no sum
+                               // (a sum from +0 is never -0)
+      const int sw = (tid ^ (tid >> 3)) & 15;
+#pragma unroll 2
+      for (int u = 0; u < kStatTok / 8; ++u) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(sm + tid * 512 + (u ^ sw) * 16);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += bf2f(uint16_t(w[e >> 1] >> ((e & 1) * 16)));  // token order
+      }
+    } else {
+#pragma unroll 16
+      for (int r = 0; r < rows; ++r) sum += bf2f(kst[r * D + tid]);  // sequential, token order
+    }
+    st_dev(part + (int64_t(h) * nb + b) * D + tid, sum / float(p.Skv));
+  } else if (tid < 2 * D) {
+    float am = 0.f;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) am = fmaxf(am, red[w][tid - D]);
+    st_dev(part + int64_t(p.Hkv) * nb * D + (int64_t(h) * nb + b) * D + (tid - D), am);
+  }
+  wait_vm();
+  __syncthreads();
+  if (tid == 0)
+    __hip_atomic_store(flg + int64_t(h) * nb + b, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  MX_STAMP(2);
+
+  // ---- K mean and V abs-max of the head: every work-group folds the partials ----
+  float s = 0.f, am = 0.f;
+  fused_fold<D>(k, v, p, h, nb, part, flg, epoch, wait_ticks, sm, miss, s, am);
+  if (b == 0 && tid < D) {
+    km[h * D + tid] = s;
+    va[h * D + tid] = am;
+  }
+  if (tid < D) {
+    kms[tid] = s;
+    vas[tid] = am;
+  }
+  __syncthreads();  // also: every read of the K rows in sm is done
+  MX_STAMP(3);
+
+  // ---- K - mean -> INT8, one scale per 64-key tile (threads [128 tl, 128 tl + 128)) ----
+  const int tl = tid / TPT;
+  const int64_t key0 = t0 + tl * kKvPad;  // first key of this thread's tile
+  float mean[8], vsc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    mean[j] = kms[c * 8 + j];
+    const float a = vas[c * 8 + j];
+    vsc[j] = a > 0.f ? 448.f / a : 0.f;
+  }
+  auto kx = [&](int i, int j) __attribute__((always_inline)) {
+    return r0 + i < rows ? bf2f(uint16_t(kr[i][j >> 1] >> ((j & 1) * 16))) - mean[j] : 0.f;
+  };
+  float tam = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPT; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) tam = fmaxf(tam, fabsf(kx(i, j)));
+  tam = wave_max(tam);
+  float* tred = &red[0][0];
+  if (lane == 0) tred[wave] = tam;
+
+  // ---- V -> e4m3 into the V^T tile in LDS: channel row d, RPT-byte granule of
+  // tokens r0.. at granule (r0 / RPT) ^ ((c & 7) << GSH), which spreads a wave's
+  // writes over every bank ----
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float f[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      f[i] = r0 + i < rows && vsc[j] > 0.f ? bf2f(uint16_t(vr[i][j >> 1] >> ((j & 1) * 16))) * vsc[j] : 0.f;
+    const int d = c * 8 + j, gi = (r0 / RPT) ^ ((c & 7) << GSH);
+    unsigned char* dst = sm + d * kStatTok + gi * RPT;
+    if constexpr (RPT == 8)
+      *reinterpret_cast<u32x2*>(dst) = u32x2{e4m3x2_sat(f[0], f[1]) | (e4m3x2_sat(f[2], f[3]) << 16),
+                                             e4m3x2_sat(f[4], f[5]) | (e4m3x2_sat(f[6], f[7]) << 16)};
+    else
+      *reinterpret_cast<uint32_t*>(dst) = e4m3x2_sat(f[0], f[1]) | (e4m3x2_sat(f[2], f[3]) << 16);
+  }
+  __syncthreads();
+  tam = fmaxf(tred[2 * tl], tred[2 * tl + 1]);
+  const float inv = tam > 0.f ? 127.f / tam : 0.f;
+  if (key0 < skv_pad) {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = kx(i, j);
+      *reinterpret_cast<u32x2*>(ki + (int64_t(h) * skv_pad + t0 + r0 + i) * D + c * 8) = quant8(x, inv);
+    }
+    if ((tid & (TPT - 1)) == 0) ks[int64_t(h) * (skv_pad / kKvPad) + key0 / kKvPad] = tam / 127.f * 1.f;
+    // tile table entry (as prep_kv_quant): liveness bits, K scale negated when a key is dead
+    if ((tid & (TPT - 1)) < 64) {
+      const int64_t key = key0 + lane;
+      const bool live = key < p.Skv && (!p.kv_valid || p.kv_valid[key]);
+      const uint64_t bits = __ballot(live);
+      if (lane == 0)
+        tab[int64_t(h) * (skv_pad / kKvPad + 1) + key0 / kKvPad] =
+            u32x4{uint32_t(bits), uint32_t(bits >> 32),
+                  __float_as_uint(bits == ~0ull ? tam / 127.f : -(tam / 127.f)), 0u};
+    }
+  }
+  // ---- V^T rows: channel d, the block's keys below skv_pad, 16 bytes per thread ----
+  const int nkeys = int(skv_pad - t0 < kStatTok ? skv_pad - t0 : kStatTok);
+  for (int i = tid; i < D * (kStatTok / 16); i += NT) {
+    const int d = i / (kStatTok / 16), u = i % (kStatTok / 16);
+    if (u * 16 >= nkeys) continue;
+    const int gi = (u * (16 / RPT)) ^ (((d >> 3) & 7) << GSH);
+    *reinterpret_cast<u32x4*>(vt + (int64_t(h) * D + d) * skv_pad + t0 + u * 16) =
+        *reinterpret_cast<const u32x4*>(sm + d * kStatTok + gi * RPT);
+  }
+#ifdef MX_STAMPS
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  MX_STAMP(4);
+#endif
 }
 
 // ---------------- main kernel ----------------
@@ -1152,6 +1499,20 @@ SagePlan sage_plan(const mx_attn_params& p) {
   return pl;
 }
 
+// Epoch of one fused-prologue call: a per-process counter from a random start, never 0
+// (a zeroed workspace holds no set flag).
+uint64_t next_epoch() {
+  static std::atomic<uint64_t> ctr{[] {
+    std::random_device rd;
+    return (uint64_t(rd()) << 32) ^ uint64_t(rd()) ^
+           uint64_t(std::chrono::steady_clock::now().time_since_epoch().count());
+  }()};
+  uint64_t e;
+  do e = ctr.fetch_add(1, std::memory_order_relaxed);
+  while (e == 0);
+  return e;
+}
+
 mx_sage_layout sage_layout(const mx_attn_params& p) {
   mx_sage_layout L{};
   const SagePlan pl = sage_plan(p);
@@ -1178,6 +1539,7 @@ mx_sage_layout sage_layout(const mx_attn_params& p) {
   L.tab = take(16 * size_t(p.Hkv) * size_t(L.skv_pad / kKvPad + 1));
   L.split = take(sizeof(float) * split_floats(sage_shape(p).nw, p.D) * size_t(pl.units) * pl.parts);
   L.cnt = take(sizeof(int) * size_t(pl.units));
+  L.flg = take(sizeof(uint64_t) * size_t(p.Hkv) * size_t(nb));
   L.total = off;
   return L;
 }
@@ -1219,6 +1581,30 @@ hipError_t sage_quantize_d(const uint16_t* q, const uint16_t* k, const uint16_t*
     stats = q_group == 64 ? prep_stats_q<D, -1, 64> : prep_stats_q<D, -1, 16>;
     kvq = prep_kv_quant<D, -1>;
   }
+  // one-pass K/V prologue (prep_kv_fused) for the plain prologue outside stream capture
+#ifdef MX_STAMPS
+  const bool debug_old = std::getenv("MX_DEBUG_OLD_PROLOGUE") != nullptr;  // debug builds: A/B of the two paths
+#else
+  constexpr bool debug_old = false;
+#endif
+  if (mode < 0 && nb <= kFoldNb && !debug_old) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const hipError_t ce = hipStreamIsCapturing(s, &cap);
+    if (ce != hipSuccess) return ce;
+    if (cap == hipStreamCaptureStatusNone) {
+      hipLaunchKernelGGL(prep_kv_fused<D>, dim3(unsigned(int64_t(p.Hkv) * nb)), dim3(512), 0, s, k, v, p, nb,
+                         L.skv_pad, part, km, va, reinterpret_cast<int8_t*>(ws + L.ki),
+                         reinterpret_cast<float*>(ws + L.ks), reinterpret_cast<uint8_t*>(ws + L.vt),
+                         reinterpret_cast<u32x4*>(ws + L.tab), reinterpret_cast<int*>(ws + L.cnt), L.split_units,
+                         reinterpret_cast<uint64_t*>(ws + L.flg), next_epoch(),
+                         g_fused_wait_ticks.load(std::memory_order_relaxed));
+      if (!skip_q && qgroups > 0)  // Q blocks only (no statistics blocks: nb = 0)
+        hipLaunchKernelGGL(stats, dim3(unsigned((qgroups + 3) / 4)), dim3(256), 0, s, q, k, v, p, 0, qmult,
+                           L.sq_pad, part, reinterpret_cast<int8_t*>(ws + L.qi), reinterpret_cast<float*>(ws + L.qs),
+                           nq, nk);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL(stats, dim3(unsigned(blocks1)), dim3(256), 0, s, q, k, v, p, nb, qmult, L.sq_pad, part,
                      reinterpret_cast<int8_t*>(ws + L.qi), reinterpret_cast<float*>(ws + L.qs), nq, nk);
   // up to kFoldNb statistics partials per head (Skv <= 8192) the K/V quantizer sums
@@ -1234,6 +1620,8 @@ hipError_t sage_quantize_d(const uint16_t* q, const uint16_t* k, const uint16_t*
                      reinterpret_cast<int*>(ws + L.cnt), L.split_units, reinterpret_cast<u32x4*>(ws + L.tab));
   return hipGetLastError();
 }
+
+void set_prologue_wait_ticks(uint64_t ticks) { g_fused_wait_ticks.store(ticks, std::memory_order_relaxed); }
 
 hipError_t launch_sage_quantize(const uint16_t* q, const uint16_t* k, const uint16_t* v, const mx_attn_params& p,
                                 char* ws, hipStream_t s, const NormRope* nr, int q_group) {
