@@ -1483,12 +1483,36 @@ SagePlan sage_plan(const mx_attn_params& p) {
   if (U64 >= 0x7fffffff) return pl;
   const int U = int(U64), r = U % C;
   if (r == 0) return pl;
-  double best = 1.0;
-  for (int S = 2; S <= kMaxParts && S * 4 <= nt; ++S) {  // parts of >= 4 key tiles
-    const double cost = double((int64_t(r) * S + C - 1) / C) / S;
-    if (cost < best - 1e-9) best = cost, pl.parts = S;
+  if (sh.per_cu == 2 && U <= C) {
+    // The whole grid is one dispatch round: estimate the call's time for each part
+    // count S (parts of >= 4 key tiles) from rates measured on an MI355X (D = 128 pipe
+    // kernel, us): a work-group alone on its CU runs a 64-key tile in ~0.62, two
+    // co-resident ones ~1.1 each; launch + set-up + finish ~7; a split adds its
+    // partial stores and merge, ~4 + 0.75 S. Parts beyond the 512 slots run in further
+    // rounds, each paying the set-up again. Unsplit wins wherever the parts would
+    // only double up on CUs (e.g. 216 units of 17 tiles: 18 against 24 us split in
+    // two); long units on few CUs still split (128 units of 32 tiles: 2 parts).
+    double best = 0.0;
+    for (int S = 1; S <= kMaxParts && (S == 1 || S * 4 <= nt); ++S) {
+      const int64_t P = int64_t(U) * S;
+      const double w = double(nt) / S;
+      const int rounds = int((P + C - 1) / C);
+      double t = 7.0 + (S > 1 ? 4.0 + 0.75 * S : 0.0);
+      if (P <= kNominalCUs) t += w * 0.62;
+      else t += rounds * w * 1.1 + (rounds - 1) * 7.0;
+      if (S == 1 || t < best - 1e-9) best = t, pl.parts = S;
+    }
+    if (pl.parts > 1) pl.full = 0, pl.units = U;
+  } else {
+    // Several rounds: split the last round's r units into S parts, S minimising the
+    // round count of the parts per part, ceil(r S / C) / S
+    double best = 1.0;
+    for (int S = 2; S <= kMaxParts && S * 4 <= nt; ++S) {  // parts of >= 4 key tiles
+      const double cost = double((int64_t(r) * S + C - 1) / C) / S;
+      if (cost < best - 1e-9) best = cost, pl.parts = S;
+    }
+    if (pl.parts > 1) pl.full = U - r, pl.units = r;
   }
-  if (pl.parts > 1) pl.full = U - r, pl.units = r;
 #ifdef MX_STAMPS
   if (const char* e = getenv("MX_SAGE_PARTS")) {  // debug builds: force the part count
     const int S = atoi(e);

@@ -115,6 +115,14 @@ def test_workspace_and_layout():
     assert L["split_qt"] == 128 and L["split_units"] == 304 and L["split_parts"] == 3
     assert L["total"] < 45e6 + 4 * (nw * 2176) * L["split_units"] * L["split_parts"]
     assert L["cnt"] - L["split"] >= 4 * (nw * 2176) * L["split_units"] * L["split_parts"]
+    # grids of one dispatch round (<= 512 units): split only where the parts spread over
+    # idle CUs enough to pay for their merge (measured on the box, µs: 1088 x 24 heads
+    # 18 unsplit / 22 in two parts; 2048 x 24: 42 / 45; 2048 x 8: 26 / 23; 1024 x 2: 4 parts)
+    for (S, H), parts in {(1088, 24): 1, (2048, 24): 1, (512, 24): 1, (2048, 8): 2, (1024, 2): 4}.items():
+        Lp = sage_layout(AttnParams(Sq=S, Skv=S if S != 1024 else 4352, Hq=H, Hkv=H, D=128))
+        assert Lp["split_parts"] == parts, (S, H, Lp["split_parts"])
+        units = (S + 127) // 128 * H
+        assert Lp["split_units"] == (units if parts > 1 else 0)
     p2 = AttnParams(Sq=1000, Skv=77, Hq=4, Hkv=2, D=128)
     L2 = sage_layout(p2)
     assert L2["sq_pad"] == 1024 and L2["skv_pad"] == 128

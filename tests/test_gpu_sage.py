@@ -336,24 +336,25 @@ def test_split_units_dead_parts_and_repeat(cuda):
 
 def test_split_repeat_across_shapes(cuda):
     """Two split plans sharing one workspace in alternation (config 3: 304 units x 3
-    parts; config 1: 216 units x 2 parts, the partial regions overlap): every call of
-    a shape reproduces that shape's first output bit for bit, so no call reads
-    partials or counters another call left behind."""
+    parts after a full round; 2048 x 8 heads: all 128 units x 2 parts, the partial
+    regions overlap): every call of a shape reproduces that shape's first output bit
+    for bit, so no call reads partials or counters another call left behind."""
     outs, ins = {}, {}
     ws = None
-    for cid in (3, 1):
-        c = CONFIGS[cid]
-        q, k, v, m = make_inputs(c, seed=cid, device=cuda)
-        p = AttnParams(Sq=c.S, Skv=c.S, Hq=c.H, Hkv=c.H, D=128, kv_valid=m)
+    c = CONFIGS[3]
+    q, k, v, m = make_inputs(c, seed=3, device=cuda)
+    ins[3] = (q, k, v, AttnParams(Sq=c.S, Skv=c.S, Hq=c.H, Hkv=c.H, D=128, kv_valid=m))
+    q, k, v, *_ = _bias_inputs(2048, 2048, 8, 8, 128, 0, 2.0, cuda, 41)
+    ins["2048x8"] = (q, k, v, AttnParams(Sq=2048, Skv=2048, Hq=8, Hkv=8, D=128))
+    for cid, (q, k, v, p) in ins.items():
         L = sage_layout(p)
-        print(f"config {cid}: split units {L['split_units']} parts {L['split_parts']}", flush=True)
+        print(f"{cid}: split units {L['split_units']} parts {L['split_parts']}", flush=True)
         assert L["split_parts"] > 1
-        ins[cid] = (q, k, v, p)
         n = flash_attn_fp8_workspace(p)
         ws = n if ws is None else max(ws, n)
     ws = torch.empty(ws, dtype=torch.uint8, device=cuda)
     for rep in range(3):
-        for cid in (3, 1):
+        for cid in ins:
             q, k, v, p = ins[cid]
             o = torch.empty_like(q)
             flash_attn_fp8(q, k, v, o, p, ws)
