@@ -1527,9 +1527,13 @@ SagePlan sage_plan(const mx_attn_params& p) {
 // (a zeroed workspace holds no set flag).
 uint64_t next_epoch() {
   static std::atomic<uint64_t> ctr{[] {
-    std::random_device rd;
-    return (uint64_t(rd()) << 32) ^ uint64_t(rd()) ^
-           uint64_t(std::chrono::steady_clock::now().time_since_epoch().count());
+    uint64_t x = uint64_t(std::chrono::steady_clock::now().time_since_epoch().count()) * 0x9E3779B97F4A7C15ull;
+    try {  // no entropy source: the clock alone (a start value only needs to differ between processes)
+      std::random_device rd;
+      x ^= (uint64_t(rd()) << 32) ^ uint64_t(rd());
+    } catch (...) {
+    }
+    return x;
   }()};
   uint64_t e;
   do e = ctr.fetch_add(1, std::memory_order_relaxed);
