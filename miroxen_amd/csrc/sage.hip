@@ -25,7 +25,9 @@ namespace {
 
 // ---------------- prologue ----------------
 //
-// Three launches (the reference uses a memset and four kernels, :433-446):
+// Eager calls with Skv <= 8192 (plain prologue) run prep_kv_fused, one launch over K
+// and V (below), plus prep_stats_q's Q blocks when Q is quantized here. Otherwise
+// three launches (the reference uses a memset and four kernels, :433-446):
 //  1. prep_stats_q: blocks [0, Hkv*nb) reduce K/V statistics of one 256-token
 //     block of one head; the remaining blocks quantize Q (one 16-row group per
 //     wave). K/V rows are staged through LDS with 16-byte coalesced loads, then
