@@ -1505,6 +1505,18 @@ SagePlan sage_plan(const mx_attn_params& p) {
       if (S == 1 || t < best - 1e-9) best = t, pl.parts = S;
     }
     if (pl.parts > 1) pl.full = 0, pl.units = U;
+  } else if (sh.per_cu == 1 && U <= C) {
+    // The same for the 8-wave kernel (D = 64; one work-group per CU): ~1.0 us per tile,
+    // ~3.5 us of set-up per round of parts, a split ~4.5 (measured: 192 units of 32
+    // tiles 39 us unsplit against 44 in four parts; 120 units of 17 tiles 21 in two
+    // parts against 23 unsplit)
+    double best = 0.0;
+    for (int S = 1; S <= kMaxParts && (S == 1 || S * 4 <= nt); ++S) {
+      const int rounds = int((int64_t(U) * S + C - 1) / C);
+      const double t = 7.0 + (S > 1 ? 4.5 : 0.0) + rounds * (double(nt) / S + 3.5);
+      if (S == 1 || t < best - 1e-9) best = t, pl.parts = S;
+    }
+    if (pl.parts > 1) pl.full = 0, pl.units = U;
   } else {
     // Several rounds: split the last round's r units into S parts, S minimising the
     // round count of the parts per part, ceil(r S / C) / S
