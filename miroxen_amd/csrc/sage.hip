@@ -534,8 +534,13 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))
   static_assert(D == 64 || D == 128, "head dimension 64 or 128");
   constexpr int NT = 512, CPR = D / 8, RPT = kStatTok * CPR / NT;  // chunks per row, tokens per thread
   constexpr int TPT = kKvPad / RPT * CPR;                           // threads per 64-key tile (128)
-  constexpr int G = kStatTok / RPT, GSH = D == 128 ? 2 : 3;         // V^T granules per row, swizzle shift
-  static_assert(TPT == 128 && G / 8 == (1 << GSH), "layout");
+  static_assert(TPT == 128, "layout");
+  // V^T granule swizzle of channel chunk cc: D = 128 (32 granules of 8 bytes per row; a
+  // 32-lane pass of 8-byte writes covers 16 chunks x 2 granules): (cc & 15) << 1; D = 64
+  // (64 granules of 4 bytes; a 64-lane pass covers 8 chunks x 8 granules): cc << 3. Both
+  // give every lane of a pass its own bank pair / bank and keep each 16-byte read's
+  // granules adjacent and in order.
+  auto vsw = [](int cc) __attribute__((always_inline)) { return D == 128 ? (cc & 15) << 1 : (cc & 7) << 3; };
   __shared__ __align__(16) unsigned char sm[kStatTok * D * 2];  // K rows, then V^T
   __shared__ float red[NT / 64][D];
   __shared__ float kms[D], vas[D];
@@ -668,7 +673,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))
   if (lane == 0) tred[wave] = tam;
 
   // ---- V -> e4m3 into the V^T tile in LDS: channel row d, RPT-byte granule of
-  // tokens r0.. at granule (r0 / RPT) ^ ((c & 7) << GSH), which spreads a wave's
+  // tokens r0.. at granule (r0 / RPT) ^ vsw(c), which spreads a wave's
   // writes over every bank ----
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -676,7 +681,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))
 #pragma unroll
     for (int i = 0; i < RPT; ++i)
       f[i] = r0 + i < rows && vsc[j] > 0.f ? bf2f(uint16_t(vr[i][j >> 1] >> ((j & 1) * 16))) * vsc[j] : 0.f;
-    const int d = c * 8 + j, gi = (r0 / RPT) ^ ((c & 7) << GSH);
+    const int d = c * 8 + j, gi = (r0 / RPT) ^ vsw(c);
     unsigned char* dst = sm + d * kStatTok + gi * RPT;
     if constexpr (RPT == 8)
       *reinterpret_cast<u32x2*>(dst) = u32x2{e4m3x2_sat(f[0], f[1]) | (e4m3x2_sat(f[2], f[3]) << 16),
@@ -712,7 +717,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))
   for (int i = tid; i < D * (kStatTok / 16); i += NT) {
     const int d = i / (kStatTok / 16), u = i % (kStatTok / 16);
     if (u * 16 >= nkeys) continue;
-    const int gi = (u * (16 / RPT)) ^ (((d >> 3) & 7) << GSH);
+    const int gi = (u * (16 / RPT)) ^ vsw(d >> 3);
     *reinterpret_cast<u32x4*>(vt + (int64_t(h) * D + d) * skv_pad + t0 + u * 16) =
         *reinterpret_cast<const u32x4*>(sm + d * kStatTok + gi * RPT);
   }
