@@ -148,3 +148,39 @@ def test_fused_prologue_recompute_path(cuda):
             assert np.array_equal(_tab(ws1, p, L), _tab(ws2, p, L))
     finally:
         _lib.check(lib.mx_sage_prologue_wait_ticks(20000))
+
+
+def _random_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        Skv = int(rng.integers(1, 8193))
+        Hkv = int(rng.choice([1, 2, 3, 4]))
+        Hq = Hkv * int(rng.choice([1, 2]))
+        D = int(rng.choice([64, 128]))
+        out.append((int(rng.integers(1, 600)), Skv, Hq, Hkv, D, int(rng.choice([0, 3, 8])),
+                    float(rng.choice([0.0, 2.0, 8.0])), bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_cases(8, 2026), ids=_case_id)
+def test_fused_prologue_random_shapes(cuda, case):
+    """Seeded random shapes on the one-pass path (Skv <= 8192): every workspace region
+    equals the oracle's restatement of the reference quantizer."""
+    Sq, Skv, Hq, Hkv, D, pad, kbias, masked = case
+    print(f"random fused prologue {_case_id(case)}", flush=True)
+    q, k, v, qs, ks = _bias_inputs(Sq, Skv, Hq, Hkv, D, pad, kbias, cuda, Skv + 13 * Sq)
+    mask = None
+    if masked:
+        mask = (torch.rand(Skv, generator=torch.Generator().manual_seed(Skv)) > 0.3).to(torch.uint8).to(cuda)
+    p = AttnParams(Sq=Sq, Skv=Skv, Hq=Hq, Hkv=Hkv, D=D, q_stride=qs, kv_stride=ks, o_stride=qs, kv_valid=mask)
+    L = sage_layout(p)
+    ws = _ws(p, cuda)
+    ws.fill_(0x5A)
+    sage_quantize(q, k, v, p, ws)
+    torch.cuda.synchronize()
+    got = _quantized(ws, p, L)
+    _, want = oracle.sage_reference(_bits(q), _bits(k), _bits(v), Sq, Skv, Hq, Hkv, D, q_stride=qs, kv_stride=ks,
+                                    rows=np.zeros(0, np.int32))
+    for name in REGIONS:
+        assert np.array_equal(got[name], want[name]), f"{name} differs from the reference quantizer"
