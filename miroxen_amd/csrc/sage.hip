@@ -645,7 +645,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))
   }
   if (tid < D) {
     kms[tid] = s;
-    vas[tid] = am;
+    vas[tid] = am > 0.f ? 448.f / am : 0.f;  // the channel's V scale, one division per channel
   }
   __syncthreads();  // also: every read of the K rows in sm is done
   MX_STAMP(3);
@@ -655,19 +655,24 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))
   const int64_t key0 = t0 + tl * kKvPad;  // first key of this thread's tile
   float mean[8], vsc[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    mean[j] = kms[c * 8 + j];
-    const float a = vas[c * 8 + j];
-    vsc[j] = a > 0.f ? 448.f / a : 0.f;
-  }
-  auto kx = [&](int i, int j) __attribute__((always_inline)) {
-    return r0 + i < rows ? bf2f(uint16_t(kr[i][j >> 1] >> ((j & 1) * 16))) - mean[j] : 0.f;
+  for (int j = 0; j < 8; ++j) mean[j] = kms[c * 8 + j], vsc[j] = vas[c * 8 + j];
+  // rows past Skv (loaded as zeros) give 0; a whole block (every block but a head's
+  // last, usually) takes the version without the row test (FULL)
+  const bool full = rows == kStatTok;
+  auto kx = [&](int i, int j, auto fullc) __attribute__((always_inline)) {
+    const float x = bf2f(uint16_t(kr[i][j >> 1] >> ((j & 1) * 16))) - mean[j];
+    if constexpr (decltype(fullc)::value) return x;
+    else return r0 + i < rows ? x : 0.f;
   };
-  float tam = 0.f;
+  auto k_amax = [&](auto fullc) __attribute__((always_inline)) {
+    float m = 0.f;
 #pragma unroll
-  for (int i = 0; i < RPT; ++i)
+    for (int i = 0; i < RPT; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) tam = fmaxf(tam, fabsf(kx(i, j)));
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(kx(i, j, fullc)));
+    return m;
+  };
+  float tam = full ? k_amax(std::true_type{}) : k_amax(std::false_type{});
   tam = wave_max(tam);
   float* tred = &red[0][0];
   if (lane == 0) tred[wave] = tam;
@@ -677,10 +682,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))
   // writes over every bank ----
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
+    // rows past Skv are zeros (0 * vsc = +0); a channel with no nonzero value stays 0
     float f[RPT];
+    const bool live = vsc[j] > 0.f;
 #pragma unroll
-    for (int i = 0; i < RPT; ++i)
-      f[i] = r0 + i < rows && vsc[j] > 0.f ? bf2f(uint16_t(vr[i][j >> 1] >> ((j & 1) * 16))) * vsc[j] : 0.f;
+    for (int i = 0; i < RPT; ++i) {
+      const float x = bf2f(uint16_t(vr[i][j >> 1] >> ((j & 1) * 16))) * vsc[j];
+      f[i] = live ? x : 0.f;
+    }
     const int d = c * 8 + j, gi = (r0 / RPT) ^ vsw(c);
     unsigned char* dst = sm + d * kStatTok + gi * RPT;
     if constexpr (RPT == 8)
@@ -693,13 +702,17 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))
   tam = fmaxf(tred[2 * tl], tred[2 * tl + 1]);
   const float inv = tam > 0.f ? 127.f / tam : 0.f;
   if (key0 < skv_pad) {
+    auto k_store = [&](auto fullc) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      float x[8];
+      for (int i = 0; i < RPT; ++i) {
+        float x[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = kx(i, j);
-      *reinterpret_cast<u32x2*>(ki + (int64_t(h) * skv_pad + t0 + r0 + i) * D + c * 8) = quant8(x, inv);
-    }
+        for (int j = 0; j < 8; ++j) x[j] = kx(i, j, fullc);
+        *reinterpret_cast<u32x2*>(ki + (int64_t(h) * skv_pad + t0 + r0 + i) * D + c * 8) = quant8(x, inv);
+      }
+    };
+    if (full) k_store(std::true_type{});
+    else k_store(std::false_type{});
     if ((tid & (TPT - 1)) == 0) ks[int64_t(h) * (skv_pad / kKvPad) + key0 / kKvPad] = tam / 127.f * 1.f;
     // tile table entry (as prep_kv_quant): liveness bits, K scale negated when a key is dead
     if ((tid & (TPT - 1)) < 64) {
